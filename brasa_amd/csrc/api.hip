@@ -1,0 +1,241 @@
+// C ABI of libbrasa_attn.so: argument validation mirroring the reference's asserts, the error
+// plumbing, and the device plumbing of brasa_hip_rt.h. Kernels live in kv.hip, decode.hip and
+// prefill.hip.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/brasa_hip_rt.h"
+#include "common.hpp"
+
+namespace brasa {
+
+int store_kv_launch(int kv, const float* src, void* dst, size_t n, hipStream_t stream);
+int dequant_q8_launch(const void* src, float* dst, size_t rows, hipStream_t stream);
+int fill_u8_launch(void* dst, uint8_t value, size_t bytes, hipStream_t stream);
+int fill_normal_launch(float* out, size_t n, uint64_t seed, float scale, hipStream_t stream);
+int decode_launch(const float* q, const void* k, const void* v, float* partials, void* o,
+                  int o_f16, int hq, int hkv, int lk, int kv, bool per_head, hipStream_t stream);
+int prefill_launch(const float* q, const void* k, const void* v, void* o, int tokens, int hq,
+                   int hkv, int pos0, int kv, int precision, hipStream_t stream);
+
+namespace {
+thread_local char g_err[512] = "";
+}
+
+int set_error(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return set_error(BRASA_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+    return BRASA_OK;
+}
+
+static int hip_ok(hipError_t e, const char* what) {
+    if (e != hipSuccess) return set_error(BRASA_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+    return BRASA_OK;
+}
+
+static inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+static bool valid_kv(int kv) {
+    return kv == BRASA_KV_F32 || kv == BRASA_KV_F16 || kv == BRASA_KV_Q8_0;
+}
+
+// Largest sizes the kernels index with 32-bit integers.
+static constexpr size_t kMaxPositions = (size_t)1 << 30;
+static constexpr size_t kMaxHeads = 1024;
+
+}  // namespace brasa
+
+using namespace brasa;
+
+extern "C" {
+
+size_t brasa_decode_partials_len(size_t hq, size_t lk) {
+    return hq * ((lk + BRASA_DECODE_CHUNK - 1) / BRASA_DECODE_CHUNK) * 130;
+}
+
+int brasa_gqa_supported(size_t hq, size_t hkv) {
+    if (hkv == 0 || hq % hkv != 0) return 0;
+    const size_t g = hq / hkv;
+    return g == 1 || g == 2 || g == 4 || g == 8;
+}
+
+size_t brasa_kv_bytes(int kv, size_t n) {
+    switch (kv) {
+        case BRASA_KV_F32: return n * 4;
+        case BRASA_KV_F16: return n * 2;
+        case BRASA_KV_Q8_0:
+            if (n % kDim != 0) {
+                set_error(BRASA_ERR_SHAPE, "KV Q8: rows of %d values (n = %zu)", kDim, n);
+                return 0;
+            }
+            return n / kDim * kQ8Row;
+    }
+    set_error(BRASA_ERR_ARG, "invalid kv type %d", kv);
+    return 0;
+}
+
+int brasa_store_kv(int kv, const float* src, void* dst, size_t n, void* stream) {
+    g_err[0] = 0;
+    if (!valid_kv(kv)) return set_error(BRASA_ERR_ARG, "store_kv: invalid kv type %d", kv);
+    if (n == 0) return BRASA_OK;
+    if (!src || !dst) return set_error(BRASA_ERR_ARG, "store_kv: null pointer");
+    if (kv == BRASA_KV_Q8_0 && n % kDim != 0)  // lib.rs:1039
+        return set_error(BRASA_ERR_SHAPE, "KV Q8: rows of %d values (n = %zu)", kDim, n);
+    return store_kv_launch(kv, src, dst, n, as_stream(stream));
+}
+
+int brasa_dequantize_kv_q8(const void* src, float* dst, size_t rows, void* stream) {
+    g_err[0] = 0;
+    if (rows == 0) return BRASA_OK;
+    if (!src || !dst) return set_error(BRASA_ERR_ARG, "dequantize_kv_q8: null pointer");
+    return dequant_q8_launch(src, dst, rows, as_stream(stream));
+}
+
+static int decode_common(const float* q, const void* k, const void* v, float* partials,
+                         size_t partials_len, void* o, int o_dtype, brasa_attn_shape s,
+                         void* stream, bool per_head) {
+    g_err[0] = 0;
+    if (!valid_kv(s.kv)) return set_error(BRASA_ERR_ARG, "decode: invalid kv type %d", s.kv);
+    if (o_dtype != BRASA_OUT_F32 && o_dtype != BRASA_OUT_F16)
+        return set_error(BRASA_ERR_ARG, "decode: invalid output dtype %d", o_dtype);
+    // lib.rs:1074-1080 / 1128-1135
+    if (s.tokens != 1) return set_error(BRASA_ERR_SHAPE, "decode_attention is for one token");
+    if (s.dim != (size_t)kDim)
+        return set_error(BRASA_ERR_SHAPE, "decode_attention requires head_dim 128");
+    if (s.hkv == 0 || s.hq % s.hkv != 0)
+        return set_error(BRASA_ERR_SHAPE, "hq must be a multiple of hkv");
+    if (s.hq > kMaxHeads || s.pos0 + 1 > kMaxPositions)
+        return set_error(BRASA_ERR_SHAPE, "decode: shape too large");
+    const size_t lk = s.pos0 + 1;
+    if (partials_len < brasa_decode_partials_len(s.hq, lk))
+        return set_error(BRASA_ERR_SCRATCH, "decode scratch too small (%zu < %zu floats)",
+                         partials_len, brasa_decode_partials_len(s.hq, lk));
+    if (!per_head && !brasa_gqa_supported(s.hq, s.hkv))
+        return set_error(BRASA_ERR_UNSUPPORTED,
+                         "decode_attention_lanes: GQA group %zu not compiled", s.hq / s.hkv);
+    if (!q || !k || !v || !partials || !o) return set_error(BRASA_ERR_ARG, "decode: null pointer");
+    return decode_launch(q, k, v, partials, o, o_dtype == BRASA_OUT_F16, (int)s.hq, (int)s.hkv,
+                         (int)lk, s.kv, per_head, as_stream(stream));
+}
+
+int brasa_decode_attention_lanes(const float* q, const void* k, const void* v, float* partials,
+                                 size_t partials_len, void* o, int o_dtype,
+                                 brasa_attn_shape shape, void* stream) {
+    return decode_common(q, k, v, partials, partials_len, o, o_dtype, shape, stream, false);
+}
+
+int brasa_decode_attention(const float* q, const void* k, const void* v, float* partials,
+                           size_t partials_len, void* o, int o_dtype, brasa_attn_shape shape,
+                           void* stream) {
+    return decode_common(q, k, v, partials, partials_len, o, o_dtype, shape, stream, true);
+}
+
+int brasa_flash_attention_with(const float* q, const void* k, const void* v, void* o,
+                               brasa_attn_shape s, int precision, void* stream) {
+    g_err[0] = 0;
+    if (!valid_kv(s.kv)) return set_error(BRASA_ERR_ARG, "flash_attention: invalid kv %d", s.kv);
+    if (precision != BRASA_PREFILL_F16 && precision != BRASA_PREFILL_F32 &&
+        precision != BRASA_PREFILL_F16_PF32)
+        return set_error(BRASA_ERR_ARG, "flash_attention: invalid precision %d", precision);
+    // lib.rs:1203-1204
+    if (s.dim != (size_t)kDim)
+        return set_error(BRASA_ERR_SHAPE, "flash_attention requires head_dim 128");
+    if (s.hkv == 0 || s.hq % s.hkv != 0)
+        return set_error(BRASA_ERR_SHAPE, "hq must be a multiple of hkv");
+    if (s.hq > kMaxHeads || s.pos0 + s.tokens + BRASA_KV_ALIGN > kMaxPositions)
+        return set_error(BRASA_ERR_SHAPE, "flash_attention: shape too large");
+    if (s.tokens == 0) return BRASA_OK;
+    if (!q || !k || !v || !o) return set_error(BRASA_ERR_ARG, "flash_attention: null pointer");
+    return prefill_launch(q, k, v, o, (int)s.tokens, (int)s.hq, (int)s.hkv, (int)s.pos0, s.kv,
+                          precision, as_stream(stream));
+}
+
+int brasa_flash_attention(const float* q, const void* k, const void* v, void* o,
+                          brasa_attn_shape shape, void* stream) {
+    return brasa_flash_attention_with(q, k, v, o, shape, BRASA_PREFILL_F16, stream);
+}
+
+const char* brasa_last_error(void) { return g_err; }
+
+const char* brasa_version(void) { return "brasa_attn 0.1.0 (gfx950)"; }
+
+// ---- device plumbing (brasa_hip_rt.h) -----------------------------------------------------
+
+int brasa_rt_device_count(int* count) { return hip_ok(hipGetDeviceCount(count), "hipGetDeviceCount"); }
+int brasa_rt_set_device(int device) { return hip_ok(hipSetDevice(device), "hipSetDevice"); }
+int brasa_rt_device_name(char* buf, size_t len) {
+    hipDeviceProp_t p;
+    int dev = 0;
+    int st = hip_ok(hipGetDevice(&dev), "hipGetDevice");
+    if (st) return st;
+    st = hip_ok(hipGetDeviceProperties(&p, dev), "hipGetDeviceProperties");
+    if (st) return st;
+    snprintf(buf, len, "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
+    return BRASA_OK;
+}
+int brasa_rt_malloc(void** ptr, size_t bytes) { return hip_ok(hipMalloc(ptr, bytes), "hipMalloc"); }
+int brasa_rt_free(void* ptr) { return hip_ok(hipFree(ptr), "hipFree"); }
+int brasa_rt_memcpy_htod(void* dst, const void* src, size_t bytes) {
+    return hip_ok(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+}
+int brasa_rt_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
+    return hip_ok(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+}
+int brasa_rt_memcpy_dtod(void* dst, const void* src, size_t bytes, void* stream) {
+    return hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)),
+                  "hipMemcpyAsync D2D");
+}
+int brasa_rt_fill_u8(void* dst, uint8_t value, size_t bytes, void* stream) {
+    return fill_u8_launch(dst, value, bytes, as_stream(stream));
+}
+int brasa_rt_device_synchronize(void) {
+    return hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize");
+}
+int brasa_rt_stream_create(void** stream) {
+    hipStream_t s = nullptr;
+    int st = hip_ok(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+    *stream = s;
+    return st;
+}
+int brasa_rt_stream_destroy(void* stream) {
+    return hip_ok(hipStreamDestroy(as_stream(stream)), "hipStreamDestroy");
+}
+int brasa_rt_stream_synchronize(void* stream) {
+    return hip_ok(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize");
+}
+int brasa_rt_event_create(void** event) {
+    hipEvent_t e = nullptr;
+    int st = hip_ok(hipEventCreate(&e), "hipEventCreate");
+    *event = e;
+    return st;
+}
+int brasa_rt_event_destroy(void* event) {
+    return hip_ok(hipEventDestroy(static_cast<hipEvent_t>(event)), "hipEventDestroy");
+}
+int brasa_rt_event_record(void* event, void* stream) {
+    return hip_ok(hipEventRecord(static_cast<hipEvent_t>(event), as_stream(stream)),
+                  "hipEventRecord");
+}
+int brasa_rt_event_elapsed_ms(float* ms, void* start, void* stop) {
+    return hip_ok(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start),
+                                      static_cast<hipEvent_t>(stop)),
+                  "hipEventElapsedTime");
+}
+int brasa_rt_event_synchronize(void* event) {
+    return hip_ok(hipEventSynchronize(static_cast<hipEvent_t>(event)), "hipEventSynchronize");
+}
+int brasa_rt_fill_normal_f32(float* out, size_t n, uint64_t seed, float scale, void* stream) {
+    return fill_normal_launch(out, n, seed, scale, as_stream(stream));
+}
+
+}  // extern "C"

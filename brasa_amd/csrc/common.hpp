@@ -1,0 +1,122 @@
+// Shared device helpers for the gfx950 attention kernels: KV-row access per cache type, f16
+// conversion, wave64 cross-lane reductions and the error plumbing of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <cstdlib>
+
+#include "../../include/brasa_attn.h"
+
+namespace brasa {
+
+constexpr int kDim = 128;        // head_dim (the reference asserts 128 on every attention path)
+constexpr int kQ8Row = 136;      // 128 int8 + 4 f16 scales
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---- host-side error plumbing -------------------------------------------------------------
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+// ---- f16 helpers --------------------------------------------------------------------------
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return static_cast<float>(__ushort_as_half(h));
+}
+// v_cvt_f16_f32: round to nearest even, overflow to inf, f16 subnormals kept.
+__device__ __forceinline__ uint16_t f2h(float f) {
+    return __half_as_ushort(__float2half_rn(f));
+}
+
+// ---- DPP / cross-lane helpers (wave64) ----------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// Sum over the 16 lanes of a DPP row with a butterfly of xor masks 15, 7, 3, 1 (row_mirror,
+// row_half_mirror, quad_perm [3,2,1,0], quad_perm [1,0,3,2]). Partners add the same two values,
+// so every lane of the row ends with identical bits.
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp<0x140>(x);
+    x += dpp<0x141>(x);
+    x += dpp<0x1B>(x);
+    x += dpp<0xB1>(x);
+    return x;
+}
+__device__ __forceinline__ float shfl_xor(float x, int mask) {
+    return __shfl_xor(x, mask, 64);
+}
+
+// ---- KV row access ------------------------------------------------------------------------
+// Cache element types, one per KvType value.
+template <int KV> struct KvTraits;
+template <> struct KvTraits<BRASA_KV_F32> { static constexpr int row_bytes = 512; };
+template <> struct KvTraits<BRASA_KV_F16> { static constexpr int row_bytes = 256; };
+template <> struct KvTraits<BRASA_KV_Q8_0> { static constexpr int row_bytes = kQ8Row; };
+
+// Eight consecutive values [d0, d0 + 8) of a cache row, in their storage form. For q8_0 the
+// values are the raw int8 codes and `scale` is the f16 scale of their 32-group (exact product:
+// value = scale * code, as dequantize_kv_q8).
+template <int KV> struct Kv8;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+// Streaming loads: K/V rows are read once per kernel, so they should not displace reused data.
+template <typename T>
+__device__ __forceinline__ T ld_stream(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const T*>(p));
+}
+
+template <> struct Kv8<BRASA_KV_F16> {
+    u32x4 raw;
+    __device__ __forceinline__ void load(const uint8_t* row, int d0) {
+        raw = ld_stream<u32x4>(row + 2 * d0);
+    }
+    __device__ __forceinline__ void to_float(float (&x)[8]) const {
+        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x[2 * i] = h2f(static_cast<uint16_t>(w[i] & 0xffffu));
+            x[2 * i + 1] = h2f(static_cast<uint16_t>(w[i] >> 16));
+        }
+    }
+    __device__ __forceinline__ float scale() const { return 1.0f; }
+};
+
+template <> struct Kv8<BRASA_KV_F32> {
+    f32x4 a, b;
+    __device__ __forceinline__ void load(const uint8_t* row, int d0) {
+        a = ld_stream<f32x4>(row + 4 * d0);
+        b = ld_stream<f32x4>(row + 4 * d0 + 16);
+    }
+    __device__ __forceinline__ void to_float(float (&x)[8]) const {
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    }
+    __device__ __forceinline__ float scale() const { return 1.0f; }
+};
+
+template <> struct Kv8<BRASA_KV_Q8_0> {
+    u32x2 raw;
+    uint16_t sc;
+    __device__ __forceinline__ void load(const uint8_t* row, int d0) {
+        // rows are 136 bytes: 8-byte aligned, so the 8 codes are one dwordx2
+        raw = ld_stream<u32x2>(row + d0);
+        sc = *reinterpret_cast<const uint16_t*>(row + 128 + 2 * (d0 >> 5));
+    }
+    __device__ __forceinline__ void to_float(float (&x)[8]) const {
+        const uint32_t w[2] = {raw.x, raw.y};
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                x[4 * i + b] = static_cast<float>(static_cast<int8_t>((w[i] >> (8 * b)) & 0xffu));
+        }
+    }
+    __device__ __forceinline__ float scale() const { return h2f(sc); }
+};
+
+}  // namespace brasa

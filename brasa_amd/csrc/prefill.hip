@@ -1,0 +1,345 @@
+// Causal flash-attention prefill on gfx950 MFMA.
+//
+// Behaviour follows Kernels::flash_attention_with (crates/kernels/src/lib.rs:1185-1248;
+// flash_attention.metal:152-323): query t of the chunk sits at absolute position pos0 + t and
+// attends to keys [0, pos0 + t]; softmax and accumulation in f32. PrefillPrecision::F16 rounds
+// Q * scale (computed in f32) to f16 and writes f16 output (flash_attention.metal:213,320);
+// ::F32 keeps Q and output in f32.
+//
+// Design for MI355X (dense contraction on the matrix cores):
+//   * workgroup = 4 wave64 sharing one KV head: the HW (<= 4) query heads of a GQA group times
+//     32 * 4 / HW query tokens; every wave owns 32 queries of one head, so the 4 waves of a
+//     G = 4 group read each K/V tile from LDS once per head instead of from HBM;
+//   * S^T = K Q^T and O^T = V^T P^T with v_mfma_f32_32x32x16_f16: the S^T accumulator layout
+//     (lane = query column, 16 keys per lane) is exactly the B-operand layout P^T needs, so P
+//     never goes through LDS; K is read from LDS row-major, V is stored transposed in LDS
+//     (d-major) so each A operand is two ds_read_b64;
+//   * 64-key K/V tiles, global loads for tile i+1 issued before the MFMAs of tile i;
+//   * causal skipping per wave (32-key sub-blocks past its last query are not computed) and
+//     masking only on sub-blocks that cross the diagonal; heaviest query tiles dispatch first
+//     (flash_attention.metal:202-205) and the head-group index varies fastest so the 8 KV heads
+//     spread over the 8 XCDs (each XCD's L2 keeps its head's K/V);
+//   * values that f16 cannot hold exactly (f32 and q8_0 caches, f32 Q, f32 P) are split as
+//     x = hi + lo with hi = f16(x), lo = f16(x - hi) and contracted with extra MFMAs
+//     (hi*hi + hi*lo + lo*hi), which keeps ~22 significant bits.
+#include "common.hpp"
+
+namespace brasa {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 256;
+constexpr int kTile = 64;       // keys per LDS tile
+constexpr int kKStr = 136;      // K row stride in halves (128 + 8 pad)
+constexpr int kVStr = 72;       // V^T row stride in halves (64 + 8 pad)
+
+struct PrefillArgs {
+    const float* q;
+    const uint8_t* k;
+    const uint8_t* v;
+    void* o;
+    int tokens, hq, hkv, group, pos0;
+    int ntiles;                 // query tiles
+    float scale;
+};
+
+
+__device__ __forceinline__ void split_f16(float x, uint16_t& hi, uint16_t& lo) {
+    hi = f2h(x);
+    lo = f2h(x - h2f(hi));
+}
+
+__device__ __forceinline__ half8 lds_b128(const uint16_t* p) {
+    return __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(p));
+}
+__device__ __forceinline__ half8 lds_2xb64(const uint16_t* p0, const uint16_t* p1) {
+    uint2 a = *reinterpret_cast<const uint2*>(p0);
+    uint2 b = *reinterpret_cast<const uint2*>(p1);
+    uint4 c = make_uint4(a.x, a.y, b.x, b.y);
+    return __builtin_bit_cast(half8, c);
+}
+__device__ __forceinline__ half8 pack8(const uint16_t (&x)[8]) {
+    uint4 c;
+    c.x = x[0] | ((uint32_t)x[1] << 16);
+    c.y = x[2] | ((uint32_t)x[3] << 16);
+    c.z = x[4] | ((uint32_t)x[5] << 16);
+    c.w = x[6] | ((uint32_t)x[7] << 16);
+    return __builtin_bit_cast(half8, c);
+}
+
+__device__ __forceinline__ f32x16 mfma(half8 a, half8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// KV = cache type; HW = query heads per workgroup (1, 2, 4); QS = split Q (F32 precision);
+// PS = split P; OF32 = f32 output.
+template <int KV, int HW, bool QS, bool PS, bool OF32>
+__global__ void __launch_bounds__(kThreads, 2)
+prefill_kernel(PrefillArgs a) {
+    constexpr bool KS = (KV != BRASA_KV_F16);  // cache values need hi/lo
+    constexpr int NK = KS ? 2 : 1;
+    constexpr int TPW = 32 * 4 / HW;            // query tokens per workgroup
+    constexpr int RB = KvTraits<KV>::row_bytes;
+
+    __shared__ __attribute__((aligned(16))) uint16_t s_k[NK][kTile * kKStr];
+    __shared__ __attribute__((aligned(16))) uint16_t s_vt[NK][kDim * kVStr];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int col = lane & 31;       // query column of the MFMA tiles
+    const int u = lane >> 5;         // lane half
+
+    const int hg = blockIdx.x;                            // head group (fastest: spreads XCDs)
+    const int tile = a.ntiles - 1 - (int)blockIdx.y;      // heaviest query tiles first
+    const int h = hg * HW + (wave % HW);
+    const int kh = (hg * HW) / a.group;
+    const int t0 = tile * TPW;
+    const int tw0 = t0 + 32 * (wave / HW);                // first query token of this wave
+    const int lk = a.pos0 + a.tokens;
+    const int kend_wg = a.pos0 + min(t0 + TPW, a.tokens);  // keys [0, kend_wg) are read
+    const int kend_w = a.pos0 + min(tw0 + 32, a.tokens);   // this wave needs [0, kend_w)
+
+    // ---- Q^T B-operands: k-step t holds d = 16t + 8u + j ------------------------------
+    const int tq = tw0 + col;
+    const bool qvalid = tq < a.tokens;
+    half8 qh[8], ql[QS ? 8 : 1];
+    {
+        const float* qrow = a.q + ((size_t)(qvalid ? tq : 0) * a.hq + h) * kDim;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float4* p = reinterpret_cast<const float4*>(qrow + 16 * t + 8 * u);
+            float4 x0 = p[0], x1 = p[1];
+            float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            uint16_t hi[8], lo[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float sx = qvalid ? xs[j] * a.scale : 0.0f;
+                if (QS) split_f16(sx, hi[j], lo[j]);
+                else hi[j] = f2h(sx);
+            }
+            qh[t] = pack8(hi);
+            if (QS) ql[t] = pack8(lo);
+        }
+    }
+
+    f32x16 acc[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[dt][i] = 0.0f;
+    float m2 = -INFINITY;  // running max of s * log2(e)
+    float lsum = 0.0f;     // this lane's share of the softmax denominator
+    const int qabs = a.pos0 + tq;
+
+    // ---- global -> register staging of one 64-key tile ----------------------------------
+    // item i of thread (wave, lane): key = lane, 8-dim chunk = wave + 4 i (i = 0..3)
+    const size_t kstride = (size_t)a.hkv * RB;
+    const uint8_t* kbase = a.k + (size_t)kh * RB;
+    const uint8_t* vbase = a.v + (size_t)kh * RB;
+    Kv8<KV> rk[4], rv[4];
+    auto load_tile = [&](int kb) {
+        const size_t row = (size_t)(kb + lane) * kstride;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            rk[i].load(kbase + row, 8 * (wave + 4 * i));
+            rv[i].load(vbase + row, 8 * (wave + 4 * i));
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c8 = 8 * (wave + 4 * i);
+            float kf[8], vf[8];
+            rk[i].to_float(kf);
+            rv[i].to_float(vf);
+            const float ks = rk[i].scale(), vs = rv[i].scale();
+            uint16_t khi[8], klo[8], vhi[8], vlo[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                if (KS) {
+                    split_f16(KV == BRASA_KV_Q8_0 ? kf[e] * ks : kf[e], khi[e], klo[e]);
+                    split_f16(KV == BRASA_KV_Q8_0 ? vf[e] * vs : vf[e], vhi[e], vlo[e]);
+                } else {
+                    khi[e] = f2h(kf[e]);
+                    vhi[e] = f2h(vf[e]);
+                }
+            }
+            *reinterpret_cast<half8*>(&s_k[0][lane * kKStr + c8]) = pack8(khi);
+            if (KS) *reinterpret_cast<half8*>(&s_k[NK - 1][lane * kKStr + c8]) = pack8(klo);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                s_vt[0][(c8 + e) * kVStr + lane] = vhi[e];
+                if (KS) s_vt[NK - 1][(c8 + e) * kVStr + lane] = vlo[e];
+            }
+        }
+    };
+
+    load_tile(0);
+    for (int kb = 0; kb < kend_wg; kb += kTile) {
+        __syncthreads();  // previous tile fully consumed
+        store_tile();
+        __syncthreads();
+        if (kb + kTile < kend_wg) load_tile(kb + kTile);
+
+        if (kb >= kend_w) continue;  // this wave's queries are all before the tile
+        const int nsub = (kb + 32 < kend_w) ? 2 : 1;
+
+        // S^T for the two 32-key sub-blocks
+        f32x16 s[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[b][i] = 0.0f;
+            if (b < nsub) {
+                const uint16_t* krow = &s_k[0][(32 * b + col) * kKStr + 8 * u];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const half8 ka = lds_b128(krow + 16 * t);
+                    s[b] = mfma(ka, qh[t], s[b]);
+                    if (QS) s[b] = mfma(ka, ql[t], s[b]);
+                    if (KS) {
+                        const half8 kl = lds_b128(&s_k[NK - 1][(32 * b + col) * kKStr + 8 * u + 16 * t]);
+                        s[b] = mfma(kl, qh[t], s[b]);
+                    }
+                }
+            }
+        }
+        // scale to log2 domain, causal mask, tile max
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int kb2 = kb + 32 * b;
+            const bool need_mask = (kb2 + 31 > a.pos0 + tw0) || (kb2 + 31 >= lk);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int key = kb2 + 8 * (i / 4) + 4 * u + (i % 4);
+                float x = s[b][i] * kLog2e;
+                if (b >= nsub || (need_mask && (key > qabs || key >= lk))) x = -INFINITY;
+                s[b][i] = x;
+                tmax = fmaxf(tmax, x);
+            }
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mn = fmaxf(m2, tmax);  // finite: key 0 is visible to every query
+        const float alpha = __builtin_amdgcn_exp2f(m2 - mn);
+        m2 = mn;
+        lsum *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
+
+        // P^T B-operands and O^T += V^T P^T
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            if (b >= nsub) break;
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                uint16_t ph[8], pl[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float p = __builtin_amdgcn_exp2f(s[b][8 * st + j] - mn);
+                    lsum += p;
+                    if (PS) split_f16(p, ph[j], pl[j]);
+                    else ph[j] = f2h(p);
+                }
+                const half8 pb = pack8(ph);
+                half8 plb;
+                if (PS) plb = pack8(pl);
+                const int key0 = 32 * b + 16 * st + 4 * u;
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) {
+                    const int d = 32 * dt + col;
+                    const half8 va = lds_2xb64(&s_vt[0][d * kVStr + key0], &s_vt[0][d * kVStr + key0 + 8]);
+                    acc[dt] = mfma(va, pb, acc[dt]);
+                    if (PS) acc[dt] = mfma(va, plb, acc[dt]);
+                    if (KS) {
+                        const half8 vl = lds_2xb64(&s_vt[NK - 1][d * kVStr + key0],
+                                                   &s_vt[NK - 1][d * kVStr + key0 + 8]);
+                        acc[dt] = mfma(vl, pb, acc[dt]);
+                    }
+                }
+            }
+        }
+    }
+
+    // ---- normalise and write O[t, h, d] --------------------------------------------------
+    const float L = lsum + __shfl_xor(lsum, 32, 64);
+    if (!qvalid) return;
+    const float inv = 1.0f / L;
+    const size_t obase = ((size_t)tq * a.hq + h) * kDim;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = 32 * dt + 8 * g + 4 * u;
+            const float y0 = acc[dt][4 * g] * inv, y1 = acc[dt][4 * g + 1] * inv;
+            const float y2 = acc[dt][4 * g + 2] * inv, y3 = acc[dt][4 * g + 3] * inv;
+            if (OF32) {
+                *reinterpret_cast<float4*>(static_cast<float*>(a.o) + obase + d) =
+                    make_float4(y0, y1, y2, y3);
+            } else {
+                uint2 w;
+                w.x = (uint32_t)f2h(y0) | ((uint32_t)f2h(y1) << 16);
+                w.y = (uint32_t)f2h(y2) | ((uint32_t)f2h(y3) << 16);
+                *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.o) + obase + d) = w;
+            }
+        }
+    }
+}
+
+template <int KV, int HW, bool QS, bool PS, bool OF32>
+int launch(const PrefillArgs& a, hipStream_t stream) {
+    hipLaunchKernelGGL((prefill_kernel<KV, HW, QS, PS, OF32>), dim3(a.hq / HW, a.ntiles),
+                       dim3(kThreads), 0, stream, a);
+    return check_launch("prefill_kernel");
+}
+
+template <int KV, int HW>
+int launch_prec(const PrefillArgs& a, int precision, hipStream_t stream) {
+    switch (precision) {
+        case BRASA_PREFILL_F32: return launch<KV, HW, true, true, true>(a, stream);
+        case BRASA_PREFILL_F16_PF32: return launch<KV, HW, false, true, false>(a, stream);
+        default: return launch<KV, HW, false, false, false>(a, stream);
+    }
+}
+
+template <int KV>
+int launch_kv(PrefillArgs& a, int precision, hipStream_t stream) {
+    const int HW = (a.group % 4 == 0) ? 4 : (a.group % 2 == 0) ? 2 : 1;
+    const int tpw = 32 * 4 / HW;
+    a.ntiles = (a.tokens + tpw - 1) / tpw;
+    switch (HW) {
+        case 4: return launch_prec<KV, 4>(a, precision, stream);
+        case 2: return launch_prec<KV, 2>(a, precision, stream);
+        default: return launch_prec<KV, 1>(a, precision, stream);
+    }
+}
+
+}  // namespace
+
+int prefill_launch(const float* q, const void* k, const void* v, void* o, int tokens, int hq,
+                   int hkv, int pos0, int kv, int precision, hipStream_t stream) {
+    PrefillArgs a;
+    a.q = q;
+    a.k = static_cast<const uint8_t*>(k);
+    a.v = static_cast<const uint8_t*>(v);
+    a.o = o;
+    a.tokens = tokens;
+    a.hq = hq;
+    a.hkv = hkv;
+    a.group = hq / hkv;
+    a.pos0 = pos0;
+    a.ntiles = 0;
+    a.scale = 1.0f / sqrtf(static_cast<float>(kDim));
+    switch (kv) {
+        case BRASA_KV_F32: return launch_kv<BRASA_KV_F32>(a, precision, stream);
+        case BRASA_KV_F16: return launch_kv<BRASA_KV_F16>(a, precision, stream);
+        case BRASA_KV_Q8_0: return launch_kv<BRASA_KV_Q8_0>(a, precision, stream);
+    }
+    return set_error(BRASA_ERR_ARG, "flash_attention: invalid kv type %d", kv);
+}
+
+}  // namespace brasa

@@ -1,0 +1,150 @@
+/*
+ * brasa_attn -- MI355X (gfx950) attention hot path of the Brasa engine behind a C ABI.
+ *
+ * Each operation below replaces one method of the reference's `brasa_kernels::Kernels`
+ * (crates/kernels/src/lib.rs) for attention; a Rust shim turns a nonzero status back into the
+ * reference's `assert!` panic (shape/scratch/unsupported-group errors) or `MetalError`
+ * (device failures). Conventions shared by every entry point:
+ *
+ *   - Pointers are device pointers (hipMalloc'ed or views into such allocations). A view at a
+ *     byte offset, which the reference expresses as `Arg::Buf(buffer, offset)`
+ *     (crates/metal/src/runtime.rs:255-295), is passed as the already-offset pointer.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream). Work is enqueued,
+ *     never waited for; ordering is the stream's, as the reference's one in-order command queue.
+ *   - No entry point allocates device memory or keeps mutable global state (the kernel table is
+ *     static). Scratch (`partials`) is caller-owned, sized by brasa_decode_partials_len().
+ *   - Return value: BRASA_OK (0) or a BRASA_ERR_* code; brasa_last_error() then describes it
+ *     (thread-local string, valid until the next call on the same thread).
+ *
+ * KV cache layout (crates/kernels/src/metal/kv_access.metal:1-9; crates/models/src/qwen3.rs:211):
+ * one layer is [cap, hkv, 128] rows; row index = position * hkv + kv_head. Row bytes: f32 512,
+ * f16 256, q8_0 136 (128 int8 followed by 4 little-endian f16 scales, one per 32 values;
+ * crates/quant/src/qtype.rs:80-83).
+ */
+#ifndef BRASA_ATTN_H
+#define BRASA_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define BRASA_OK 0
+#define BRASA_ERR_SHAPE 1       /* a shape assert of the reference would panic */
+#define BRASA_ERR_SCRATCH 2     /* partials scratch smaller than brasa_decode_partials_len */
+#define BRASA_ERR_UNSUPPORTED 3 /* GQA group / precision combination not compiled */
+#define BRASA_ERR_LAUNCH 4      /* HIP reported an error enqueueing the kernel */
+#define BRASA_ERR_ARG 5         /* null pointer or invalid enum value */
+
+/* KvType (crates/kernels/src/lib.rs:92-143); values equal the reference's `KvType as usize`. */
+#define BRASA_KV_F32 0
+#define BRASA_KV_F16 1
+#define BRASA_KV_Q8_0 2
+
+/* PrefillPrecision (crates/kernels/src/lib.rs:1311-1318). */
+#define BRASA_PREFILL_F16 0 /* Q*scale rounded to f16, output f16 (hot path) */
+#define BRASA_PREFILL_F32 1 /* exact variant: Q and output f32 */
+/* F16 inputs and output with P carried to f32 accuracy through the P.V contraction, which is
+ * what the reference's F16 kernel computes (flash_attention.metal:197 keeps P in f32). Plain
+ * BRASA_PREFILL_F16 rounds P to f16 for the matrix cores (within the 2e-3 / 1e-2 bar). */
+#define BRASA_PREFILL_F16_PF32 2
+
+/* Output element type of the decode entry points. The reference writes f32 (its `ws.attn`);
+ * f16 (RNE) is offered for callers whose next GEMM reads f16. */
+#define BRASA_OUT_F32 0
+#define BRASA_OUT_F16 1
+
+/* AttnShape (crates/kernels/src/lib.rs:1354-1364). */
+typedef struct brasa_attn_shape {
+    size_t tokens;
+    size_t hq;
+    size_t hkv;
+    size_t dim;  /* must be 128 for every attention entry point, as in the reference */
+    size_t pos0; /* absolute position of the first query token */
+    int kv;      /* BRASA_KV_* */
+} brasa_attn_shape;
+
+/* Keys per split-K tramo of the reference (DECODE_CHUNK, lib.rs:1331). */
+#define BRASA_DECODE_CHUNK 128
+/* Positions the KV cache must be readable past pos0 + tokens for prefill (KV_ALIGN,
+ * lib.rs:1350-1351). */
+#define BRASA_KV_ALIGN 64
+
+/* decode_partials_len (lib.rs:1334-1337): floats of decode scratch for hq heads and lk keys,
+ * hq * ceil(lk / 128) * 130. The kernels here use at most that many. */
+size_t brasa_decode_partials_len(size_t hq, size_t lk);
+
+/* gqa_supported (lib.rs:1323-1327): hq / hkv in {1, 2, 4, 8}. */
+int brasa_gqa_supported(size_t hq, size_t hkv);
+
+/* KvType::bytes (lib.rs:109-121): bytes of n cache elements (n a multiple of 128 for q8_0);
+ * returns 0 and sets the error for an invalid type or a ragged q8_0 count. */
+size_t brasa_kv_bytes(int kv, size_t n);
+
+/*
+ * Kernels::store_kv (lib.rs:1029-1050; device code kv.metal:6-40): converts n f32 values at
+ * `src` into the cache type at `dst`. f32: copy; f16: round to nearest even; q8_0: n must be a
+ * multiple of 128 and each 32-group is quantised bit-exactly as quantize_kv_q8
+ * (crates/quant/src/qtype.rs:85-111).
+ */
+int brasa_store_kv(int kv, const float* src, void* dst, size_t n, void* stream);
+
+/*
+ * Dequantises `rows` q8_0 rows (136 bytes each) at `src` into rows*128 f32 values at `dst`,
+ * bit-exactly as dequantize_kv_q8 (crates/quant/src/qtype.rs:113-130) and as the in-kernel
+ * accessors read them (kv_access.metal:15-27). The reference has no separate kernel for this:
+ * it is exported so the "Q8 dequantisation is bit-exact" contract can be checked on the device.
+ */
+int brasa_dequantize_kv_q8(const void* src, float* dst, size_t rows, void* stream);
+
+/*
+ * Kernels::decode_attention_lanes (lib.rs:1110-1164; device code decode_attention.metal:
+ * 108-199 + 68-84): attention of one query token at position shape.pos0 over keys
+ * [0, pos0 + 1) of the layer cache k/v, all query heads of a GQA group served from one read of
+ * each K/V row. q: [hq, 128] f32 (scaled by 1/sqrt(128) inside, in f32); o: [hq, 128] in
+ * `o_dtype`. partials: caller scratch of partials_len floats, at least
+ * brasa_decode_partials_len(hq, pos0 + 1). Requires tokens == 1, dim == 128 and
+ * hq / hkv in {1, 2, 4, 8} (BRASA_ERR_UNSUPPORTED otherwise, where the reference panics).
+ */
+int brasa_decode_attention_lanes(const float* q, const void* k, const void* v, float* partials,
+                                 size_t partials_len, void* o, int o_dtype,
+                                 brasa_attn_shape shape, void* stream);
+
+/*
+ * Kernels::decode_attention (lib.rs:1056-1103; decode_attention.metal:15-84): same contract as
+ * brasa_decode_attention_lanes, one query head per workgroup, for any hq multiple of hkv (the
+ * reference's fallback for groups outside {1, 2, 4, 8}).
+ */
+int brasa_decode_attention(const float* q, const void* k, const void* v, float* partials,
+                           size_t partials_len, void* o, int o_dtype, brasa_attn_shape shape,
+                           void* stream);
+
+/*
+ * Kernels::flash_attention_with (lib.rs:1185-1248; flash_attention.metal:152-323): causal GQA
+ * prefill. q: [tokens, hq, 128] f32; query t (absolute position pos0 + t) attends to keys
+ * [0, pos0 + t]. k/v: layer cache readable up to ceil64(pos0 + tokens) positions (values past
+ * pos0 + tokens are masked; they must be finite). o: [tokens, hq, 128], f16 bits for
+ * BRASA_PREFILL_F16 / BRASA_PREFILL_F16_PF32 (Q*scale rounded to f16 as the reference does,
+ * fp32 softmax and accumulation) or f32 for BRASA_PREFILL_F32. Requires dim == 128 and
+ * hq % hkv == 0.
+ */
+int brasa_flash_attention_with(const float* q, const void* k, const void* v, void* o,
+                               brasa_attn_shape shape, int precision, void* stream);
+
+/* Kernels::flash_attention (lib.rs:1169-1180): brasa_flash_attention_with(.., F16). */
+int brasa_flash_attention(const float* q, const void* k, const void* v, void* o,
+                          brasa_attn_shape shape, void* stream);
+
+/* Description of the last error on this thread ("" if none). */
+const char* brasa_last_error(void);
+
+/* Library version string. */
+const char* brasa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

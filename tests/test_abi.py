@@ -1,0 +1,106 @@
+"""CPU: the C ABI library loads, exports every symbol the public headers declare, and rejects
+bad calls with the reference's assert conditions before touching the device (no GPU needed).
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+import brasa_amd
+from brasa_amd import AttnShape, BrasaError, Kernels, KvType, decode_partials_len, gqa_supported
+from brasa_amd._lib import SYMBOLS, lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    names = set()
+    for h in ("brasa_attn.h", "brasa_hip_rt.h"):
+        text = open(os.path.join(ROOT, "include", h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"\b(brasa_\w+)\s*\(", text))
+    return names
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    declared = _declared()
+    assert len(declared) >= 30
+    l = ctypes.CDLL(brasa_amd.LIB_PATH)
+    for name in declared:
+        assert hasattr(l, name), name
+    assert declared == set(SYMBOLS), declared ^ set(SYMBOLS)
+
+
+def test_built_for_gfx950_only():
+    data = open(brasa_amd.LIB_PATH, "rb").read()
+    assert b"gfx950" in data
+    for other in (b"amdgcn-amd-amdhsa--gfx942", b"amdgcn-amd-amdhsa--gfx90a"):
+        assert other not in data
+
+
+def test_constants_mirror_reference():
+    # lib.rs:1323-1351
+    assert decode_partials_len(32, 16384) == 32 * 128 * 130
+    assert decode_partials_len(32, 1) == 32 * 130
+    assert decode_partials_len(32, 129) == 32 * 2 * 130
+    assert all(gqa_supported(8 * g, 8) for g in (1, 2, 4, 8))
+    assert not gqa_supported(24, 8) and not gqa_supported(32, 0) and not gqa_supported(30, 8)
+    assert KvType.F16.bytes(128) == 256 and KvType.F32.bytes(128) == 512
+    assert KvType.Q8_0.bytes(256) == 272
+    assert lib().brasa_kv_bytes(2, 256) == 272
+    assert lib().brasa_kv_bytes(2, 100) == 0
+    assert KvType.parse("q8") == KvType.Q8_0 and KvType.parse("bf16") is None
+
+
+def _err(fn):
+    with pytest.raises(BrasaError) as e:
+        fn()
+    return e.value.code
+
+
+def test_decode_asserts_without_device():
+    k = Kernels()
+    # the checks run before any pointer is dereferenced, so fake addresses are fine
+    fake = 0x1000
+
+    class P:  # partials stand-in with a byte size
+        def __init__(self, nbytes):
+            self.nbytes, self.ptr = nbytes, fake
+
+    big = P(4 * decode_partials_len(32, 1 << 20))
+    sh = lambda **kw: AttnShape(**{**dict(tokens=1, hq=32, hkv=8, dim=128, pos0=99,
+                                          kv=KvType.F16), **kw})
+    assert _err(lambda: k.decode_attention_lanes(fake, fake, fake, big, fake, sh(tokens=2))) == 1
+    assert _err(lambda: k.decode_attention_lanes(fake, fake, fake, big, fake, sh(dim=64))) == 1
+    assert _err(lambda: k.decode_attention_lanes(fake, fake, fake, big, fake, sh(hq=30))) == 1
+    assert _err(lambda: k.decode_attention_lanes(fake, fake, fake, big, fake, sh(hq=24))) == 3
+    assert _err(lambda: k.decode_attention_lanes(fake, fake, fake, P(4 * (32 * 130 - 1)), fake,
+                                                 sh(pos0=0))) == 2
+    assert _err(lambda: k.decode_attention_lanes(0, fake, fake, big, fake, sh())) == 5
+    assert "scratch" in _scratch_msg(k, fake, P)
+
+
+def _scratch_msg(k, fake, P):
+    try:
+        k.decode_attention(fake, fake, fake, P(4), fake,
+                           AttnShape(1, 32, 8, 128, 500, KvType.F16))
+    except BrasaError as e:
+        return str(e)
+    return ""
+
+
+def test_prefill_and_store_asserts_without_device():
+    k = Kernels()
+    fake = 0x1000
+    sh = AttnShape(16, 32, 8, 64, 0, KvType.F16)
+    assert _err(lambda: k.flash_attention(fake, fake, fake, fake, sh)) == 1
+    assert _err(lambda: k.flash_attention(fake, fake, fake, fake,
+                                          AttnShape(16, 30, 8, 128, 0, KvType.F16))) == 1
+    assert _err(lambda: k.flash_attention_with(fake, fake, fake, fake,
+                                               AttnShape(16, 32, 8, 128, 0, KvType.F16), 7)) == 5
+    assert _err(lambda: k.store_kv(KvType.Q8_0, fake, fake, 100)) == 1
+    assert _err(lambda: k.store_kv(9, fake, fake, 128)) == 5
+    # zero-size calls are no-ops
+    k.store_kv(KvType.F16, fake, fake, 0)
+    k.flash_attention(fake, fake, fake, fake, AttnShape(0, 32, 8, 128, 5, KvType.F16))

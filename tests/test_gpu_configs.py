@@ -1,0 +1,104 @@
+"""GPU: the BASELINE.json configurations at their full sizes, on seeded N(0, 1) inputs.
+
+Inputs: numpy PCG64 ``default_rng(seed)``; seed s -> Q, s + 1 -> K, s + 2 -> V; values drawn in
+f32 and rounded to f16 (Q is passed as f32 holding those f16 values, as the reference's decode
+and prefill take f32 Q). Q8 caches quantise the f32 draws. Prefill inputs are put through
+per-head RMSNorm (weight 1, eps 1e-6) and RoPE-NeoX (theta 1e6) first.
+
+Decode is checked in full against the oracle (the reference's 1e-5 * max|v| bar). Prefill at
+T = 2048 / 8192 and the 512-token chunk at pos0 = 16384 is checked on sampled query rows (first,
+middle and last windows; the oracle computes exactly those rows) with the BASELINE.json bar.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from brasa_amd import AttnShape, Kernels, KvType, PrefillPrecision, decode_partials_len
+from brasa_amd.device import DeviceBuffer, synchronize
+from gpu_util import DIM, HKV, HQ, KvPair, bars, f16_normal, post_norm_rope
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+@pytest.mark.parametrize("kv,lk", [(KvType.F16, 2048), (KvType.F16, 4096), (KvType.F16, 16384),
+                                   (KvType.F16, 32768), (KvType.Q8_0, 16384)])
+def test_decode_config(kv, lk):
+    seed = 1000 + lk + int(kv)
+    q = f16_normal(np.random.default_rng(seed), HQ * DIM)
+    if kv == KvType.F16:
+        kk = f16_normal(np.random.default_rng(seed + 1), lk * HKV * DIM)
+        vv = f16_normal(np.random.default_rng(seed + 2), lk * HKV * DIM)
+    else:
+        kk = np.random.default_rng(seed + 1).standard_normal(lk * HKV * DIM, dtype=np.float32)
+        vv = np.random.default_rng(seed + 2).standard_normal(lk * HKV * DIM, dtype=np.float32)
+    cache = KvPair(kv, kk, vv)
+    gq = DeviceBuffer.from_array(q)
+    part = DeviceBuffer(4 * decode_partials_len(HQ, lk))
+    o = DeviceBuffer(HQ * DIM * 4)
+    _say(f"decode config kv={kv.name_str} lk={lk}")
+    Kernels().decode_attention_lanes(gq, cache.kbuf, cache.vbuf, part, o,
+                                     AttnShape(1, HQ, HKV, DIM, lk - 1, kv))
+    synchronize()
+    got = o.download(np.float32).reshape(1, HQ, DIM)
+    want, vmax = oracle.attention(q, cache.k, cache.v, 1, HQ, HKV, DIM, lk - 1)
+    w = oracle.worst(got, want, vmax)
+    a, r = bars(got, want)
+    print(f"decode kv={kv.name_str} lk={lk}: worst {w:.2e} max-abs {a:.2e} max-rel {r:.2e}")
+    assert w <= 1e-5 and a <= 2e-3 and r <= 1e-2
+
+
+def _prefill_inputs(tokens, pos0, seed):
+    lk = pos0 + tokens
+    cap = (lk + 63) // 64 * 64
+    c, s = oracle.rope_table(1e6, DIM, cap)
+    q = oracle.round_f16(post_norm_rope(
+        np.random.default_rng(seed).standard_normal(tokens * HQ * DIM, dtype=np.float32),
+        tokens, HQ, pos0, c, s))
+    # the cache holds positions 0..cap: RMSNorm + RoPE at their own positions
+    k = oracle.round_f16(post_norm_rope(
+        np.random.default_rng(seed + 1).standard_normal(cap * HKV * DIM, dtype=np.float32),
+        cap, HKV, 0, c, s))
+    v = f16_normal(np.random.default_rng(seed + 2), cap * HKV * DIM)
+    return q, k, v
+
+
+@pytest.mark.parametrize("tokens,pos0", [(2048, 0), (8192, 0), (512, 16384)])
+def test_prefill_config(tokens, pos0):
+    q, kk, vv = _prefill_inputs(tokens, pos0, 2000 + tokens + pos0)
+    cache = KvPair(KvType.F16, kk, vv)
+    gq = DeviceBuffer.from_array(q)
+    o = DeviceBuffer(tokens * HQ * DIM * 2)
+    _say(f"prefill config T={tokens} pos0={pos0}")
+    Kernels().flash_attention(gq, cache.kbuf, cache.vbuf, o,
+                              AttnShape(tokens, HQ, HKV, DIM, pos0, KvType.F16))
+    synchronize()
+    got = oracle.f16_to_f32(o.download(np.uint16)).reshape(tokens, HQ, DIM)
+    mid = tokens // 2
+    for t0, t1 in [(0, 4), (mid, mid + 4), (tokens - 4, tokens)]:
+        want, vmax = oracle.attention(q, cache.k, cache.v, tokens, HQ, HKV, DIM, pos0, q16=True,
+                                      rows=(t0, t1))
+        a, r = bars(got[t0:t1], want[t0:t1])
+        print(f"prefill T={tokens} pos0={pos0} rows {t0}:{t1}: max-abs {a:.2e} max-rel {r:.2e}")
+        assert a <= 2e-3 and r <= 1e-2
+    assert np.all(np.isfinite(got))
+
+
+def test_prefill_config_q8_chunk():
+    tokens, pos0 = 256, 4096
+    q, kk, vv = _prefill_inputs(tokens, pos0, 77)
+    cache = KvPair(KvType.Q8_0, kk, vv)
+    gq = DeviceBuffer.from_array(q)
+    o = DeviceBuffer(tokens * HQ * DIM * 2)
+    _say("prefill q8 chunk")
+    Kernels().flash_attention(gq, cache.kbuf, cache.vbuf, o,
+                              AttnShape(tokens, HQ, HKV, DIM, pos0, KvType.Q8_0))
+    synchronize()
+    got = oracle.f16_to_f32(o.download(np.uint16)).reshape(tokens, HQ, DIM)
+    want, _ = oracle.attention(q, cache.k, cache.v, tokens, HQ, HKV, DIM, pos0, q16=True,
+                               rows=(tokens - 8, tokens))
+    a, r = bars(got[-8:], want[-8:])
+    assert a <= 2e-3 and r <= 1e-2

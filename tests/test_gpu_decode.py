@@ -1,0 +1,132 @@
+"""GPU: split-K decode attention against the f64 oracle.
+
+Mirrors crates/kernels/tests/attention.rs:112-177 (decode_case, seed 23, pos0 in
+{0, 1, 255, 256, 700, 4095, 16383} x KV {f32, f16, q8_0}), :287-345 (other GQA groups, seed 25)
+and crates/kernels/tests/launch.rs:119-168 (seed 78, lk in {1, 37, 300, 1025}); the bar is the
+reference's ``worst <= 1e-5 * max|v|`` (attention.rs:25-32, lib.rs:5-18).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from brasa_amd import AttnShape, BrasaError, Kernels, KvType, OutDType, decode_partials_len
+from brasa_amd.device import DeviceBuffer, synchronize
+from gpu_util import DIM, HKV, HQ, KvPair
+
+pytestmark = pytest.mark.gpu
+
+KVS = [KvType.F32, KvType.F16, KvType.Q8_0]
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def run_decode(k, variant, q, cache, hq, hkv, pos0, out=OutDType.F32):
+    lk = pos0 + 1
+    gq = DeviceBuffer.from_array(q)
+    part = DeviceBuffer(4 * decode_partials_len(hq, lk))
+    o = DeviceBuffer(hq * DIM * (4 if out == OutDType.F32 else 2))
+    shape = AttnShape(1, hq, hkv, DIM, pos0, cache.kv)
+    fn = k.decode_attention_lanes if variant == "lanes" else k.decode_attention
+    fn(gq, cache.kbuf, cache.vbuf, part, o, shape, out=out)
+    synchronize()
+    if out == OutDType.F32:
+        return o.download(np.float32).reshape(hq, DIM)
+    return o.download(np.uint16).reshape(hq, DIM)
+
+
+@pytest.mark.parametrize("variant", ["lanes", "per_head"])
+@pytest.mark.parametrize("kv", KVS)
+def test_decode_case(variant, kv):
+    k = Kernels()
+    rng = oracle.Rng(23)
+    w = 0.0
+    for pos0 in [0, 1, 255, 256, 700, 4095, 16383]:
+        lk = pos0 + 1
+        q = rng.vec(HQ * DIM, 2.0)
+        cache = KvPair(kv, rng.vec(lk * HKV * DIM, 2.0), rng.vec(lk * HKV * DIM, 3.0))
+        _say(f"decode {variant} kv={kv.name_str} pos0={pos0}")
+        got = run_decode(k, variant, q, cache, HQ, HKV, pos0)
+        want, vmax = oracle.attention(q, cache.k, cache.v, 1, HQ, HKV, DIM, pos0)
+        w = max(w, oracle.worst(got, want, vmax))
+    print(f"decode {variant} KV {kv.name_str}: worst / max|v| = {w:.2e}")
+    assert w <= 1e-5, w
+
+
+@pytest.mark.parametrize("kv", KVS)
+def test_decode_other_groups(kv):
+    k = Kernels()
+    rng = oracle.Rng(25)
+    for hq in [8, 16, 64]:
+        w = 0.0
+        for pos0 in [0, 300, 4095]:
+            lk = pos0 + 1
+            q = rng.vec(hq * DIM, 2.0)
+            cache = KvPair(kv, rng.vec(lk * HKV * DIM, 2.0), rng.vec(lk * HKV * DIM, 3.0))
+            _say(f"decode lanes group={hq // HKV} kv={kv.name_str} pos0={pos0}")
+            got = run_decode(k, "lanes", q, cache, hq, HKV, pos0)
+            want, vmax = oracle.attention(q, cache.k, cache.v, 1, hq, HKV, DIM, pos0)
+            w = max(w, oracle.worst(got, want, vmax))
+        assert w <= 1e-5, (hq, w)
+
+
+def test_decode_non_power_of_two_group():
+    # group 3 is outside GQA_GROUPS: lanes is rejected (the reference panics), the per-head
+    # variant serves it (lib.rs:1056-1103)
+    k = Kernels()
+    rng = oracle.Rng(27)
+    hq, hkv, pos0 = 24, 8, 777
+    q = rng.vec(hq * DIM, 2.0)
+    cache = KvPair(KvType.F16, rng.vec((pos0 + 1) * hkv * DIM, 2.0),
+                   rng.vec((pos0 + 1) * hkv * DIM, 3.0))
+    with pytest.raises(BrasaError) as e:
+        run_decode(k, "lanes", q, cache, hq, hkv, pos0)
+    assert e.value.code == 3
+    _say("decode per_head group=3")
+    got = run_decode(k, "per_head", q, cache, hq, hkv, pos0)
+    want, vmax = oracle.attention(q, cache.k, cache.v, 1, hq, hkv, DIM, pos0)
+    assert oracle.worst(got, want, vmax) <= 1e-5
+
+
+@pytest.mark.parametrize("kv", KVS)
+def test_decode_launch_seed78_and_determinism(kv):
+    k = Kernels()
+    rng = oracle.Rng(78)
+    for lk in [1, 37, 300, 1025]:
+        n = ((lk + 127) // 128 * 128) * HKV * DIM
+        cache = KvPair(kv, rng.vec(n, 2.0), rng.vec(n, 3.0))
+        q = rng.vec(HQ * DIM, 2.0)
+        _say(f"decode seed78 kv={kv.name_str} lk={lk}")
+        a = run_decode(k, "lanes", q, cache, HQ, HKV, lk - 1)
+        b = run_decode(k, "lanes", q, cache, HQ, HKV, lk - 1)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        want, vmax = oracle.attention(q, cache.k[: lk * HKV * DIM], cache.v[: lk * HKV * DIM],
+                                      1, HQ, HKV, DIM, lk - 1)
+        assert oracle.worst(a, want, vmax) <= 1e-5
+
+
+def test_decode_f16_output_is_rne_of_f32_output():
+    k = Kernels()
+    rng = oracle.Rng(31)
+    pos0 = 5000
+    q = rng.vec(HQ * DIM, 2.0)
+    cache = KvPair(KvType.F16, rng.vec((pos0 + 1) * HKV * DIM, 2.0),
+                   rng.vec((pos0 + 1) * HKV * DIM, 3.0))
+    _say("decode f16 output")
+    o32 = run_decode(k, "lanes", q, cache, HQ, HKV, pos0)
+    o16 = run_decode(k, "lanes", q, cache, HQ, HKV, pos0, out=OutDType.F16)
+    assert np.array_equal(o16, oracle.f32_to_f16(o32))
+
+
+def test_decode_scratch_too_small():
+    k = Kernels()
+    cache = KvPair(KvType.F16, np.zeros(300 * HKV * DIM, np.float32),
+                   np.zeros(300 * HKV * DIM, np.float32))
+    q = DeviceBuffer(HQ * DIM * 4)
+    o = DeviceBuffer(HQ * DIM * 4)
+    part = DeviceBuffer(4 * (decode_partials_len(HQ, 300) - 1))
+    with pytest.raises(BrasaError) as e:
+        k.decode_attention_lanes(q, cache.kbuf, cache.vbuf, part, o,
+                                 AttnShape(1, HQ, HKV, DIM, 299, KvType.F16))
+    assert e.value.code == 2

@@ -1,0 +1,112 @@
+"""GPU: causal flash-attention prefill against the f64 oracle.
+
+Mirrors crates/kernels/tests/attention.rs:34-110 (flash_attention_gqa_causal, seed 22): the
+(T, pos0) cases below, each KV type, a cache of capacity ceil64(pos0 + T) with finite garbage
+past pos0 + T. Bars:
+  * F16 (hot path, P rounded to f16 for the matrix cores): the BASELINE.json bar against the
+    reference's Q-rounded attention (attention_q16, reference.rs:129-145): max-abs <= 2e-3 and
+    max-rel <= 1e-2 (rel = |err| / max(|ref|, 0.2)); plus the reference's own bar against the
+    unrounded attention, worst <= 2e-3 * max|v| (attention.rs:107);
+  * F16_PF32 (P at f32 accuracy, the reference F16 kernel's numerics): the reference's own bar
+    worst_f16 <= 1e-5 * max|v| against attention_q16 (attention.rs:105);
+  * F32 (exact variant): worst <= 1e-5 * max|v| against attention (attention.rs:106).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from brasa_amd import AttnShape, Kernels, KvType, PrefillPrecision
+from brasa_amd.device import DeviceBuffer, synchronize
+from gpu_util import DIM, HKV, HQ, KvPair, bars
+
+pytestmark = pytest.mark.gpu
+
+KVS = [KvType.F32, KvType.F16, KvType.Q8_0]
+CASES = [(9, 0), (5, 11), (1, 0), (1, 1500), (33, 40), (64, 448), (32, 0), (100, 7)]
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def run_prefill(k, q, cache, tokens, hq, hkv, pos0, precision):
+    gq = DeviceBuffer.from_array(q)
+    f32 = precision == PrefillPrecision.F32
+    o = DeviceBuffer(tokens * hq * DIM * (4 if f32 else 2))
+    k.flash_attention_with(gq, cache.kbuf, cache.vbuf, o,
+                           AttnShape(tokens, hq, hkv, DIM, pos0, cache.kv), precision)
+    synchronize()
+    return o.download(np.float32 if f32 else np.uint16).reshape(tokens, hq, DIM)
+
+
+@pytest.mark.parametrize("kv", KVS)
+def test_flash_attention_gqa_causal(kv):
+    k = Kernels()
+    rng = oracle.Rng(22)
+    w16 = w_raw = w_pf32 = w32 = 0.0
+    mabs = mrel = 0.0
+    for tokens, pos0 in CASES:
+        lk = pos0 + tokens
+        cap = (lk + 63) // 64 * 64
+        q = rng.vec(tokens * HQ * DIM, 2.0)
+        cache = KvPair(kv, rng.vec(cap * HKV * DIM, 2.0), rng.vec(cap * HKV * DIM, 3.0))
+        ref16, vmax = oracle.attention(q, cache.k, cache.v, tokens, HQ, HKV, DIM, pos0, q16=True)
+        raw, _ = oracle.attention(q, cache.k, cache.v, tokens, HQ, HKV, DIM, pos0)
+        _say(f"prefill F16 kv={kv.name_str} T={tokens} pos0={pos0}")
+        oh = run_prefill(k, q, cache, tokens, HQ, HKV, pos0, PrefillPrecision.F16)
+        a, r = bars(oracle.f16_to_f32(oh), ref16)
+        mabs, mrel = max(mabs, a), max(mrel, r)
+        w16 = max(w16, oracle.worst_f16(oh, ref16, vmax))
+        w_raw = max(w_raw, oracle.worst(oracle.f16_to_f32(oh), raw, vmax))
+        _say(f"prefill F16_PF32 kv={kv.name_str} T={tokens} pos0={pos0}")
+        op = run_prefill(k, q, cache, tokens, HQ, HKV, pos0, PrefillPrecision.F16_PF32)
+        w_pf32 = max(w_pf32, oracle.worst_f16(op, ref16, vmax))
+        _say(f"prefill F32 kv={kv.name_str} T={tokens} pos0={pos0}")
+        o32 = run_prefill(k, q, cache, tokens, HQ, HKV, pos0, PrefillPrecision.F32)
+        w32 = max(w32, oracle.worst(o32, raw, vmax))
+    print(f"flash KV {kv.name_str}: F16 max-abs {mabs:.2e} max-rel {mrel:.2e} "
+          f"worst_f16 {w16:.2e} vs-unrounded {w_raw:.2e}; F16_PF32 {w_pf32:.2e}; F32 {w32:.2e}")
+    assert mabs <= 2e-3 and mrel <= 1e-2, (mabs, mrel)
+    assert w_raw <= 2e-3, w_raw
+    assert w_pf32 <= 1e-5, w_pf32
+    assert w32 <= 1e-5, w32
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (64, 8), (24, 8), (12, 4)])
+def test_flash_other_groups(hq, hkv):
+    k = Kernels()
+    rng = oracle.Rng(29)
+    for tokens, pos0 in [(70, 0), (33, 100)]:
+        lk = pos0 + tokens
+        cap = (lk + 63) // 64 * 64
+        q = rng.vec(tokens * hq * DIM, 2.0)
+        cache = KvPair(KvType.F16, rng.vec(cap * hkv * DIM, 2.0), rng.vec(cap * hkv * DIM, 3.0))
+        _say(f"prefill group={hq // hkv} hq={hq} T={tokens} pos0={pos0}")
+        o32 = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F32)
+        raw, vmax = oracle.attention(q, cache.k, cache.v, tokens, hq, hkv, DIM, pos0)
+        assert oracle.worst(o32, raw, vmax) <= 1e-5
+        oh = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
+        ref16, _ = oracle.attention(q, cache.k, cache.v, tokens, hq, hkv, DIM, pos0, q16=True)
+        a, r = bars(oracle.f16_to_f32(oh), ref16)
+        assert a <= 2e-3 and r <= 1e-2
+
+
+def test_flash_masks_garbage_past_lk():
+    # positions in [lk, cap) hold large finite garbage; results must not depend on it
+    k = Kernels()
+    rng = oracle.Rng(33)
+    tokens, pos0 = 37, 90
+    lk = pos0 + tokens
+    cap = (lk + 63) // 64 * 64
+    q = rng.vec(tokens * HQ * DIM, 2.0)
+    kv_k = rng.vec(cap * HKV * DIM, 2.0)
+    kv_v = rng.vec(cap * HKV * DIM, 3.0)
+    a = KvPair(KvType.F16, kv_k, kv_v)
+    kv_k2, kv_v2 = kv_k.copy(), kv_v.copy()
+    kv_k2[lk * HKV * DIM:] = 6e4
+    kv_v2[lk * HKV * DIM:] = -6e4
+    b = KvPair(KvType.F16, kv_k2, kv_v2)
+    _say("prefill garbage past lk")
+    oa = run_prefill(k, q, a, tokens, HQ, HKV, pos0, PrefillPrecision.F16)
+    ob = run_prefill(k, q, b, tokens, HQ, HKV, pos0, PrefillPrecision.F16)
+    assert np.array_equal(oa, ob)
