@@ -10,7 +10,7 @@ import os
 import subprocess
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libbrasa_attn.so")
+LIB_PATH = os.environ.get("BRASA_ATTN_LIB") or os.path.join(_HERE, "libbrasa_attn.so")
 CSRC = os.path.join(_HERE, "csrc")
 
 SZ = ctypes.c_size_t

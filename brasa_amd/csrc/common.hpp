@@ -29,6 +29,13 @@ __device__ __forceinline__ float h2f(uint16_t h) {
 __device__ __forceinline__ uint16_t f2h(float f) {
     return __half_as_ushort(__float2half_rn(f));
 }
+// Materialises x as an f32 register value. The backend otherwise folds f16(a * b) into one
+// v_fma_mixlo_f16 (a single rounding of the exact product), whereas the reference rounds the
+// product to f32 first and then to f16. The empty asm emits no instruction.
+__device__ __forceinline__ float as_f32(float x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
 
 // ---- DPP / cross-lane helpers (wave64) ----------------------------------------------------
 template <int CTRL>
@@ -64,6 +71,7 @@ template <int KV> struct Kv8;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 // Streaming loads: K/V rows are read once per kernel, so they should not displace reused data.
 template <typename T>
 __device__ __forceinline__ T ld_stream(const uint8_t* p) {

@@ -1,4 +1,4 @@
-// Split-K decode attention for gfx950 (one query token per sequence).
+// Split-K decode attention for gfx950 (one query token per sequence), one kernel per call.
 //
 // Behaviour follows Kernels::decode_attention_lanes / decode_attention of the reference
 // (crates/kernels/src/lib.rs:1056-1164; decode_attention.metal:15-199): keys [0, lk) of one
@@ -7,44 +7,174 @@
 // o = sum_s w_s acc_s / sum_s w_s l_s with w_s = exp(m_s - max m).
 //
 // Design for MI355X (HBM-bound: every K/V byte is read once per GQA group):
-//   * workgroup = 4 wave64 = (split, KV head); the G query heads of the group are all served
-//     from one read of each K/V row, the rows never leave registers;
-//   * lane layout: lane = 16 * r + c holds dims [8c, 8c + 8) of key row (4i + r) of a 32-key
-//     block, so a 16-lane DPP row reads one 256 B f16 row with one 128-bit load per lane and
-//     the wave reads 4 rows per load instruction (fully coalesced);
-//   * QK: 8 FMAs per lane per head, then a 16-lane DPP butterfly (bit-identical in all lanes);
-//   * online softmax in fp32 with exp2 (v_exp_f32); per-row partial sums l/acc are only merged
-//     across rows (xor 16/32 shuffles) once per wave, then across the 4 waves through LDS;
-//   * q8_0: the 8 int8 codes of a lane share one f16 scale (8 | 32), so the scale is applied
-//     once to the lane's partial dot (as decode_attention.metal:148-162 does per block) and
-//     folded into p for P.V; dequantised values are exact (scale * code in f32);
-//   * when one split covers all keys the first kernel normalises and writes o directly.
+//   * workgroup = 4 wave64 = (split, KV head); a wave streams 32-key blocks of its split with the
+//     next block's K/V loads in flight while the current one is computed;
+//   * S^T = K Q^T on v_mfma_f32_16x16x32_f16. K rows go from HBM straight into the A operand
+//     (lane = key row, 8 contiguous dims: 16-byte loads, no conversion for f16 caches). The
+//     B operand holds the G query heads as columns, Q*scale split as hi + lo f16 (two MFMAs),
+//     so the scores keep f32 accuracy (the reference computes them in f32);
+//   * the S^T accumulator layout (lane = head column, 4 keys per lane) is used as the P^T
+//     B operand as it stands; P is split hi + lo as well. O^T += V^T P^T on the same MFMA, with
+//     V staged row-major in a wave-private LDS tile and read transposed by ds_read_tr16_b64;
+//   * online softmax in fp32 (exp2 domain) with two xor-shuffles per block for the row max;
+//   * the 4 waves merge through LDS into one partial per (head, split); a second small kernel
+//     merges the splits (an in-kernel "last workgroup merges" protocol was measured slower:
+//     its agent-scope release fence writes back the L2 of every workgroup's XCD);
+//   * q8_0: codes are exact in f16; K scales multiply the per-32-dim-group MFMA partials (one
+//     MFMA k-step is one group), V scales are folded into P per group; f32 caches are split
+//     hi + lo like Q.
 #include "common.hpp"
 
 namespace brasa {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kBlock = 32;  // keys per wave iteration: 8 quads of 4 rows
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
+
+// Waves per workgroup: f16 caches use 8 (2 per SIMD, so one computes while the other's loads
+// are in flight); the register-staged q8_0 / f32 paths use 4 (LDS).
+template <int KV, int G> constexpr int waves_for() { return (KV == BRASA_KV_F16 && G <= 4) ? 8 : 4; }
+constexpr int kBlock = 32;        // keys per wave iteration
+constexpr int kVStr = 144;        // V tile row stride in halves (256 B + 32 B pad)
+constexpr int kMaxSplits = 256;   // splits per call (their (m, l) sit in LDS during the merge)
 
 struct DecodeArgs {
     const float* q;       // [hq, 128]
     const uint8_t* k;     // layer cache base
     const uint8_t* v;
-    float* part_acc;      // [hq, splits, 128]
-    float* part_ml;       // [hq, splits, 2]
-    void* o;              // [hq, 128] (used when splits == 1)
+    float* part;          // caller scratch (arrival words, then partials)
+    void* o;              // [hq, 128]
     int o_f16;
     int hq, hkv, group;   // group = hq / hkv
     int lk, chunk, splits;
     float scale;
 };
 
+__device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ half8 as_half8(u32x4 x) { return __builtin_bit_cast(half8, x); }
+__device__ __forceinline__ uint32_t pack2(uint16_t a, uint16_t b) { return a | ((uint32_t)b << 16); }
+
+// x = hi + lo with hi = f16(x), lo = f16(x - hi): ~22 significant bits through f16 MFMAs.
+__device__ __forceinline__ void split8(const float (&x)[8], half8& hi, half8& lo) {
+    u32x4 h, l;
+    uint16_t hh[8], ll[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        hh[j] = f2h(x[j]);
+        ll[j] = f2h(x[j] - h2f(hh[j]));
+    }
+    h.x = pack2(hh[0], hh[1]); h.y = pack2(hh[2], hh[3]); h.z = pack2(hh[4], hh[5]); h.w = pack2(hh[6], hh[7]);
+    l.x = pack2(ll[0], ll[1]); l.y = pack2(ll[2], ll[3]); l.z = pack2(ll[4], ll[5]); l.w = pack2(ll[6], ll[7]);
+    hi = as_half8(h);
+    lo = as_half8(l);
+}
+
+// 8 int8 codes -> 8 f16 values (exact: |code| <= 127).
+__device__ __forceinline__ half8 codes_to_half8(u32x2 c) {
+    u32x4 r;
+    uint32_t w[2] = {c.x, c.y};
+    uint16_t h[8];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+            h[4 * i + b] = __half_as_ushort(__int2half_rn((int)(int8_t)((w[i] >> (8 * b)) & 0xffu)));
+    r.x = pack2(h[0], h[1]); r.y = pack2(h[2], h[3]); r.z = pack2(h[4], h[5]); r.w = pack2(h[6], h[7]);
+    return as_half8(r);
+}
+
+// One cache chunk of 8 consecutive dims as MFMA operand data: hi (and lo for f32 caches).
+template <int KV> struct Chunk;
+template <> struct Chunk<BRASA_KV_F16> {
+    static constexpr bool kSplit = false;
+    u32x4 raw;
+    __device__ __forceinline__ void load(const uint8_t* row, int d) { raw = ld_stream<u32x4>(row + 2 * d); }
+    __device__ __forceinline__ void get(half8& hi, half8&) const { hi = as_half8(raw); }
+};
+template <> struct Chunk<BRASA_KV_Q8_0> {
+    static constexpr bool kSplit = false;
+    u32x2 raw;
+    __device__ __forceinline__ void load(const uint8_t* row, int d) { raw = ld_stream<u32x2>(row + d); }
+    __device__ __forceinline__ void get(half8& hi, half8&) const { hi = codes_to_half8(raw); }
+};
+template <> struct Chunk<BRASA_KV_F32> {
+    static constexpr bool kSplit = true;
+    f32x4 a, b;
+    __device__ __forceinline__ void load(const uint8_t* row, int d) {
+        a = ld_stream<f32x4>(row + 4 * d);
+        b = ld_stream<f32x4>(row + 4 * d + 16);
+    }
+    __device__ __forceinline__ void get(half8& hi, half8& lo) const {
+        const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        split8(x, hi, lo);
+    }
+};
+
+// 16-byte HBM -> LDS copy per lane (global_load_lds_dwordx4): lane i writes lds + 16 i.
+// M0 (the LDS base) is saved and restored around it. Issued as inline asm so that the compiler's vector-memory counter bookkeeping never relies on
+// it (its own waits can only become more conservative); the wait before the LDS reads of such
+// a tile is wait_vmcnt below.
+__device__ __forceinline__ void lds_dma16(const uint8_t* src, uint16_t* lds_wave_base) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)lds_wave_base);
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(src), "s"(m0)
+        : "memory");
+}
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited), then a compiler memory barrier.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+    asm volatile("" ::: "memory");
+}
+
+// Per-block register state of one wave: K fragments (2 key tiles x 4 dim steps), V chunks
+// (8 rows of 4 per lane), and for q8_0 the f16 scales of the rows each lane needs.
+template <int KV> struct Block {
+    Chunk<KV> k[2][4];
+    Chunk<KV> v[8];
+    u32x2 ksc[2][4];   // q8_0: scales of S rows 16 kt + 4 u + i
+    u32x2 vsc[8];      // q8_0: scales of P slot keys kappa(u, j)
+    uint16_t vrs[8];   // q8_0: scale of V chunk i (row 4 i + u, group c16 / 4)
+};
+
+// A q8_0 scale s is applied as 2^e * (s * 2^-e), e = min(exponent(s), 9) (-14 for f16
+// subnormals): 2^e goes into the f16 V codes (code * 2^e is exact in f16 for |code| <= 127) and
+// the mantissa part into P, so P * mantissa keeps its hi/lo split clear of f16 subnormals.
+__device__ __forceinline__ int q8_exp(uint16_t sc) {
+    const int e = (int)((sc >> 10) & 31u);
+    return e == 0 ? -14 : min(e - 15, 9);
+}
+
 template <int KV, int G>
-__global__ void __launch_bounds__(kThreads)
-decode_split_kernel(DecodeArgs a) {
+__global__ void __launch_bounds__((64 * waves_for<KV, G>()), 1)
+decode_kernel(DecodeArgs a) {
     constexpr int RB = KvTraits<KV>::row_bytes;
+    constexpr bool KS = Chunk<KV>::kSplit;
+    constexpr bool Q8 = (KV == BRASA_KV_Q8_0);
+    constexpr int NV = KS ? 2 : 1;
+    constexpr int kWaves = waves_for<KV, G>();
+    constexpr int kThreads = 64 * kWaves;
+    // f16 caches: V rows go HBM -> LDS directly (global_load_lds_dwordx4), double-buffered,
+    // 16-byte chunks XOR-swizzled by 2 * (row & 3) so the transposed reads are conflict-free.
+    // Other caches: V goes through registers (conversion), one padded tile (+ lo tile for f32).
+    constexpr bool DMA = (KV == BRASA_KV_F16);
+    constexpr int kVTile = DMA ? kBlock * kDim : NV * kBlock * kVStr;
+
+    __shared__ __attribute__((aligned(16))) uint16_t s_v[kWaves][kVTile];
+    // second V buffer of the DMA path, a distinct object so the compiler can tell its loads
+    // from the first buffer's when it places waits
+    __shared__ __attribute__((aligned(16))) uint16_t s_v2[kWaves][DMA ? kBlock * kDim : 8];
     __shared__ float s_acc[kWaves][G][kDim];
     __shared__ float s_m[kWaves][G];
     __shared__ float s_l[kWaves][G];
@@ -54,130 +184,240 @@ decode_split_kernel(DecodeArgs a) {
     const int kh = h0 / a.group;           // its KV head
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int r = lane >> 4;               // key row within a quad
-    const int d0 = (lane & 15) * 8;        // first of the lane's 8 dims
+    const int c16 = lane & 15;             // MFMA row/column index
+    const int u = lane >> 4;               // MFMA k-group (8 of the 32 k-slots)
+    const bool colq = c16 < G;             // this lane's column is a query head
 
-    // Q * scale in f32 (decode_attention.metal:124)
-    float qv[G][8];
+    // ---- Q^T B-operands: column c = head h0 + c, k-step t holds dims 32 t + 8 u + j ----------
+    half8 qhi[4], qlo[4];
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-        const float4* qp = reinterpret_cast<const float4*>(a.q + (size_t)(h0 + h) * kDim + d0);
-        float4 x0 = qp[0], x1 = qp[1];
-        qv[h][0] = x0.x * a.scale; qv[h][1] = x0.y * a.scale;
-        qv[h][2] = x0.z * a.scale; qv[h][3] = x0.w * a.scale;
-        qv[h][4] = x1.x * a.scale; qv[h][5] = x1.y * a.scale;
-        qv[h][6] = x1.z * a.scale; qv[h][7] = x1.w * a.scale;
-    }
-
-    float m[G], l[G], acc[G][8];
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        m[h] = -INFINITY;
-        l[h] = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
+    for (int t = 0; t < 4; ++t) {
+        // unconditional 128-bit loads (a valid head for every lane), masked afterwards
+        const f32x4* qp = reinterpret_cast<const f32x4*>(
+            a.q + (size_t)(h0 + (colq ? c16 : 0)) * kDim + 32 * t + 8 * u);
+        const f32x4 q0 = qp[0], q1 = qp[1];
+        const float sc = colq ? a.scale : 0.0f;
+        const float x[8] = {q0.x * sc, q0.y * sc, q0.z * sc, q0.w * sc,
+                            q1.x * sc, q1.y * sc, q1.z * sc, q1.w * sc};  // f32, as reference
+        split8(x, qhi[t], qlo[t]);
     }
 
     const int s0 = split * a.chunk;
     const int s1 = min(a.lk, s0 + a.chunk);
-    const size_t kstride = (size_t)a.hkv * RB;  // bytes between consecutive positions
+    const size_t kstride = (size_t)a.hkv * RB;
     const uint8_t* kbase = a.k + (size_t)kh * RB;
     const uint8_t* vbase = a.v + (size_t)kh * RB;
+    uint16_t* vt = &s_v[wave][0];
+    uint16_t* vt2 = &s_v2[wave][0];
 
-    for (int jb = s0 + wave * kBlock; jb < s1; jb += kWaves * kBlock) {
-        Kv8<KV> kr[8], vr[8];
+    auto load = [&](Block<KV>& b, int jb, int buf) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int j = min(jb + 4 * i + r, s1 - 1);
-            kr[i].load(kbase + (size_t)j * kstride, d0);
+        for (int kt = 0; kt < 2; ++kt) {
+            const uint8_t* row = kbase + (size_t)min(jb + 16 * kt + c16, s1 - 1) * kstride;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) b.k[kt][t].load(row, 32 * t + 8 * u);
         }
+        if constexpr (DMA) {
+            // instruction i fills LDS rows 4 i .. 4 i + 3 of buffer `buf`; lane (u, p) writes
+            // physical chunk p of row 4 i + u with logical chunk p ^ 2u
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int j = min(jb + 4 * i + r, s1 - 1);
-            vr[i].load(vbase + (size_t)j * kstride, d0);
+            for (int i = 0; i < 8; ++i)
+                lds_dma16(vbase + (size_t)min(jb + 4 * i + u, s1 - 1) * kstride + 16 * (c16 ^ (2 * u)),
+                          (buf ? vt2 : vt) + 512 * i);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                b.v[i].load(vbase + (size_t)min(jb + 4 * i + u, s1 - 1) * kstride, 8 * c16);
         }
-        // scores
-        float s[8][G];
+        if constexpr (Q8) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            float kf[8];
-            kr[i].to_float(kf);
-            const float ksc = kr[i].scale();
+            for (int i = 0; i < 8; ++i)
+                b.vrs[i] = *reinterpret_cast<const uint16_t*>(
+                    vbase + (size_t)min(jb + 4 * i + u, s1 - 1) * kstride + 128 + 2 * (c16 >> 2));
+        }
+        if constexpr (Q8) {
 #pragma unroll
-            for (int h = 0; h < G; ++h) {
-                float t = 0.0f;
+            for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) t = fmaf(qv[h][e], kf[e], t);
-                t = row16_sum(t);
-                if (KV == BRASA_KV_Q8_0) t *= ksc;
-                s[i][h] = (jb + 4 * i + r < s1) ? t : -INFINITY;
+                for (int i = 0; i < 4; ++i)
+                    b.ksc[kt][i] = *reinterpret_cast<const u32x2*>(
+                        kbase + (size_t)min(jb + 16 * kt + 4 * u + i, s1 - 1) * kstride + 128);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int key = (j < 4) ? 4 * u + j : 16 + 4 * u + (j - 4);
+                b.vsc[j] = *reinterpret_cast<const u32x2*>(
+                    vbase + (size_t)min(jb + key, s1 - 1) * kstride + 128);
             }
         }
-        // online softmax update (block max over the wave's 32 keys)
+    };
+
+    float m2[1] = {-INFINITY};  // running max of the column's scores, log2 domain
+    float lsum = 0.0f;          // this lane's share of the column's softmax denominator
+    f32x4 acc[8];               // O^T rows 16 dt + 4 u + i, column c16
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float bm = s[0][h];
+    for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto compute = [&](const Block<KV>& b, int jb, int buf) {
+        // V rows -> wave-private LDS tile (row-major, 8 dims per lane and row)
 #pragma unroll
-            for (int i = 1; i < 8; ++i) bm = fmaxf(bm, s[i][h]);
-            bm = fmaxf(bm, shfl_xor(bm, 16));
-            bm = fmaxf(bm, shfl_xor(bm, 32));
-            const float mn = fmaxf(m[h], bm);  // finite: row 0 of quad 0 is always a key
-            const float alpha = __builtin_amdgcn_exp2f((m[h] - mn) * kLog2e);
-            m[h] = mn;
-            l[h] *= alpha;
+        for (int i = 0; i < (DMA ? 0 : 8); ++i) {
+            half8 hi, lo;
+            b.v[i].get(hi, lo);
+            if constexpr (Q8) {
+                const _Float16 p2 = (_Float16)__builtin_amdgcn_ldexpf(1.0f, q8_exp(b.vrs[i]));
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h][e] *= alpha;
+                for (int e = 0; e < 8; ++e) hi[e] = hi[e] * p2;  // exact: code * 2^e
+            }
+            *reinterpret_cast<half8*>(&vt[(4 * i + u) * kVStr + 8 * c16]) = hi;
+            if constexpr (KS) *reinterpret_cast<half8*>(&vt[kBlock * kVStr + (4 * i + u) * kVStr + 8 * c16]) = lo;
+        }
+        // S^T tiles: rows = keys jb + 16 kt + 4 u + i, column = head
+        float x[2][4];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float p = __builtin_amdgcn_exp2f((s[i][h] - mn) * kLog2e);
-                s[i][h] = p;
-                l[h] += p;
+        for (int kt = 0; kt < 2; ++kt) {
+            if constexpr (Q8) {
+                float sk[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    half8 kh8, unused;
+                    b.k[kt][t].get(kh8, unused);
+                    f32x4 p = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    p = mfma16(kh8, qhi[t], p);
+                    p = mfma16(kh8, qlo[t], p);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t w = (t < 2) ? b.ksc[kt][i].x : b.ksc[kt][i].y;
+                        const float sc = h2f((uint16_t)((t & 1) ? (w >> 16) : (w & 0xffffu)));
+                        sk[i] = fmaf(p[i], sc, sk[i]);  // sum over groups of (q . codes) * scale
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) x[kt][i] = sk[i];
+            } else {
+                f32x4 s = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    half8 khi, klo;
+                    b.k[kt][t].get(khi, klo);
+                    s = mfma16(khi, qhi[t], s);
+                    s = mfma16(khi, qlo[t], s);
+                    if constexpr (KS) s = mfma16(klo, qhi[t], s);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) x[kt][i] = s[i];
             }
         }
-        // P.V
+        // online softmax (exp2 domain), keys past the split masked
+        float bm = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            float vf[8];
-            vr[i].to_float(vf);
-            const float vsc = vr[i].scale();
+        for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int h = 0; h < G; ++h) {
-                const float p = (KV == BRASA_KV_Q8_0) ? s[i][h] * vsc : s[i][h];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(p, vf[e], acc[h][e]);
+            for (int i = 0; i < 4; ++i) {
+                const bool ok = jb + 16 * kt + 4 * u + i < s1;
+                x[kt][i] = ok ? x[kt][i] * kLog2e : -INFINITY;
+                bm = fmaxf(bm, x[kt][i]);
             }
+        bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+        bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+        const float mn = fmaxf(m2[0], bm);  // finite: key jb is always valid
+        const float alpha = __builtin_amdgcn_exp2f(m2[0] - mn);
+        m2[0] = mn;
+        float p[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) p[j] = __builtin_amdgcn_exp2f(x[j >> 2][j & 3] - mn);
+        float ps = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ps += p[j];
+        lsum = fmaf(lsum, alpha, ps);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+
+        // O^T += V^T P^T; P^T slot j of lane (c, u) is key kappa(u, j) = j < 4 ? 4u + j : 16 + 4u + j - 4
+        half8 phi[Q8 ? 4 : 1], plo[Q8 ? 4 : 1];
+        if constexpr (Q8) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                float pg[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t w = (g < 2) ? b.vsc[j].x : b.vsc[j].y;
+                    const uint16_t sc = (uint16_t)((g & 1) ? (w >> 16) : (w & 0xffffu));
+                    pg[j] = p[j] * __builtin_amdgcn_ldexpf(h2f(sc), -q8_exp(sc));
+                }
+                split8(pg, phi[g], plo[g]);
+            }
+        } else {
+            split8(p, phi[0], plo[0]);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        const int trc = (c16 & 3), trj = (c16 >> 2);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            const int col = 16 * dt + 4 * trc;
+            const int g = Q8 ? (dt >> 1) : 0;
+#pragma unroll
+            for (int part = 0; part < NV; ++part) {
+                const uint16_t *p1, *p2;
+                if constexpr (DMA) {
+                    // this tile's 8 DMA loads were followed by the next block's 8 K loads and
+                    // 8 DMA loads; vector-memory counts retire in order
+                    if (dt == 0) wait_vmcnt<16>();
+                    // swizzled rows of 128 halves: physical chunk = logical ^ 2 (row & 3)
+                    const uint16_t* base = buf ? vt2 : vt;
+                    const int off = ((((2 * dt + (trc >> 1)) ^ (2 * trj))) << 3) + 4 * (trc & 1);
+                    p1 = base + (4 * u + trj) * kDim + off;
+                    p2 = base + (16 + 4 * u + trj) * kDim + off;
+                } else {
+                    const uint16_t* base = vt + part * kBlock * kVStr;
+                    p1 = base + (4 * u + trj) * kVStr + col;
+                    p2 = base + (16 + 4 * u + trj) * kVStr + col;
+                }
+                const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)p1);
+                const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)p2);
+                const half8 va = __builtin_bit_cast(half8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+                acc[dt] = mfma16(va, phi[g], acc[dt]);
+                if (part == 0) acc[dt] = mfma16(va, plo[g], acc[dt]);
+            }
+        }
+    };
+
+    // ---- stream this wave's blocks: jb = s0 + 32 (wave + 4 n), next block's loads in flight --
+    const int stride = kWaves * kBlock;
+    int jb = s0 + wave * kBlock;
+    if (jb < s1) {
+        Block<KV> A, B;
+        load(A, jb, 0);
+        // the prefetch is unconditional (rows clamp to s1 - 1): a branch around it would make
+        // the compiler wait for every outstanding load before the current block's V writes
+        while (true) {
+            load(B, jb + stride, 1);
+            compute(A, jb, 0);
+            jb += stride;
+            if (jb >= s1) break;
+            load(A, jb + stride, 0);
+            compute(B, jb, 1);
+            jb += stride;
+            if (jb >= s1) break;
         }
     }
 
-    // merge the 4 key rows of the wave (lanes r = 0..3 hold disjoint keys)
+    // ---- merge the wave's 4 k-groups (disjoint keys) and the 4 waves -----------------------
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+    if (colq) {
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-        l[h] += shfl_xor(l[h], 16);
-        l[h] += shfl_xor(l[h], 32);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            acc[h][e] += shfl_xor(acc[h][e], 16);
-            acc[h][e] += shfl_xor(acc[h][e], 32);
-        }
-    }
-    if (r == 0) {
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float4* dst = reinterpret_cast<float4*>(&s_acc[wave][h][d0]);
-            dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-            dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
-        }
-        if (lane == 0) {
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                s_m[wave][h] = m[h];
-                s_l[wave][h] = l[h];
-            }
+        for (int dt = 0; dt < 8; ++dt)
+            *reinterpret_cast<f32x4*>(&s_acc[wave][c16][16 * dt + 4 * u]) = acc[dt];
+        if (u == 0) {
+            s_m[wave][c16] = m2[0];
+            s_l[wave][c16] = lsum;
         }
     }
     __syncthreads();
 
-    // merge the 4 waves (decode_attention.metal:46-65); waves without keys have m = -inf
+    const bool multi = a.splits > 1;
+    float* acc_out = a.part;
+    float* ml_out = acc_out + (size_t)a.hq * a.splits * kDim;
     for (int idx = threadIdx.x; idx < G * kDim; idx += kThreads) {
         const int h = idx / kDim, d = idx % kDim;
         float M = s_m[0][h];
@@ -186,90 +426,127 @@ decode_split_kernel(DecodeArgs a) {
         float A = 0.0f, L = 0.0f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
-            const float wt = __builtin_amdgcn_exp2f((s_m[w][h] - M) * kLog2e);
+            const float wt = __builtin_amdgcn_exp2f(s_m[w][h] - M);  // 0 for waves without keys
             A = fmaf(s_acc[w][h][d], wt, A);
             L = fmaf(s_l[w][h], wt, L);
         }
         const int hh = h0 + h;
-        if (a.splits == 1) {
+        if (!multi) {
             const float out = A / L;
-            if (a.o_f16)
-                reinterpret_cast<uint16_t*>(a.o)[hh * kDim + d] = f2h(out);
-            else
-                reinterpret_cast<float*>(a.o)[hh * kDim + d] = out;
+            if (a.o_f16) reinterpret_cast<uint16_t*>(a.o)[hh * kDim + d] = f2h(out);
+            else reinterpret_cast<float*>(a.o)[hh * kDim + d] = out;
         } else {
-            a.part_acc[((size_t)hh * a.splits + split) * kDim + d] = A;
+            acc_out[((size_t)hh * a.splits + split) * kDim + d] = A;
             if (d == 0) {
-                a.part_ml[((size_t)hh * a.splits + split) * 2] = M;
-                a.part_ml[((size_t)hh * a.splits + split) * 2 + 1] = L;
+                ml_out[((size_t)hh * a.splits + split) * 2] = M;
+                ml_out[((size_t)hh * a.splits + split) * 2 + 1] = L;
             }
         }
     }
 }
 
-// attn_decode_reduce (decode_attention.metal:68-84): one workgroup per query head, one thread
-// per dim.
-__global__ void __launch_bounds__(kDim)
-decode_reduce_kernel(const float* __restrict__ part_acc, const float* __restrict__ part_ml,
-                     void* o, int o_f16, int splits) {
-    const int h = blockIdx.x, d = threadIdx.x;
-    const float* ml = part_ml + (size_t)h * splits * 2;
-    const float* pa = part_acc + (size_t)h * splits * kDim + d;
+// Second pass (attn_decode_reduce, decode_attention.metal:68-84): one wave per (head, 32-dim
+// slice). Lane = (split subset sub = lane / 8, float4 column oi = lane % 8): every lane issues
+// all its loads at once ((m, l) and the acc float4 of splits sub, sub + 8, ...), so the pass
+// costs one memory round trip; max, denominator and the split sum are xor-shuffle reductions.
+constexpr int kRedSlice = 32;                          // dims per wave
+constexpr int kRedPer = 8;                             // splits per lane held in registers
+
+__global__ void __launch_bounds__(64)
+decode_reduce_kernel(const float* __restrict__ part, void* o, int o_f16, int hq, int splits) {
+    const int h = blockIdx.x, d0 = blockIdx.y * kRedSlice;
+    const int lane = threadIdx.x, oi = lane & 7, sub = lane >> 3;
+    const f32x4* acc = reinterpret_cast<const f32x4*>(part + (size_t)h * splits * kDim + d0) + oi;
+    const f32x2* ml = reinterpret_cast<const f32x2*>(part + (size_t)hq * splits * kDim) + (size_t)h * splits;
     float M = -INFINITY;
-    for (int s = 0; s < splits; ++s) M = fmaxf(M, ml[2 * s]);
-    float L = 0.0f, A = 0.0f;
-    for (int s = 0; s < splits; ++s) {
-        const float w = __builtin_amdgcn_exp2f((ml[2 * s] - M) * kLog2e);
-        L = fmaf(ml[2 * s + 1], w, L);
-        A = fmaf(pa[(size_t)s * kDim], w, A);
+    for (int s0 = sub; s0 < splits; s0 += 8 * kRedPer) {  // max pass over (m, l) (tiny)
+#pragma unroll
+        for (int r = 0; r < kRedPer; ++r) {
+            const int s = s0 + 8 * r;
+            if (s < splits) M = fmaxf(M, ml[s].x);
+        }
     }
-    const float out = A / L;
-    if (o_f16)
-        reinterpret_cast<uint16_t*>(o)[h * kDim + d] = f2h(out);
-    else
-        reinterpret_cast<float*>(o)[h * kDim + d] = out;
+#pragma unroll
+    for (int x = 8; x <= 32; x <<= 1) M = fmaxf(M, __shfl_xor(M, x, 64));
+    f32x4 A = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float L = 0.0f;
+    for (int s0 = sub; s0 < splits; s0 += 8 * kRedPer) {
+        f32x2 mlv[kRedPer];
+        f32x4 av[kRedPer];
+#pragma unroll
+        for (int r = 0; r < kRedPer; ++r) {
+            const int s = min(s0 + 8 * r, splits - 1);
+            mlv[r] = ml[s];
+            av[r] = acc[(size_t)s * (kDim / 4)];
+        }
+#pragma unroll
+        for (int r = 0; r < kRedPer; ++r) {
+            if (s0 + 8 * r < splits) {
+                const float w = __builtin_amdgcn_exp2f(mlv[r].x - M);
+                A += av[r] * w;
+                L = fmaf(mlv[r].y, w, L);
+            }
+        }
+    }
+#pragma unroll
+    for (int x = 8; x <= 32; x <<= 1) {
+        L += __shfl_xor(L, x, 64);
+        A.x += __shfl_xor(A.x, x, 64);
+        A.y += __shfl_xor(A.y, x, 64);
+        A.z += __shfl_xor(A.z, x, 64);
+        A.w += __shfl_xor(A.w, x, 64);
+    }
+    if (sub == 0) {
+        const float y[4] = {A.x / L, A.y / L, A.z / L, A.w / L};
+        const int off = h * kDim + d0 + 4 * oi;
+        if (o_f16) {
+            uint2 w;
+            w.x = pack2(f2h(y[0]), f2h(y[1]));
+            w.y = pack2(f2h(y[2]), f2h(y[3]));
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(o) + off) = w;
+        } else {
+            *reinterpret_cast<f32x4*>(static_cast<float*>(o) + off) = f32x4{y[0], y[1], y[2], y[3]};
+        }
+    }
 }
 
 template <int KV, int G>
-int launch_split(const DecodeArgs& a, int groups_y, hipStream_t stream) {
-    hipLaunchKernelGGL((decode_split_kernel<KV, G>), dim3(a.splits, groups_y), dim3(kThreads), 0,
-                       stream, a);
-    return check_launch("decode_split_kernel");
+int launch(const DecodeArgs& a, int groups_y, hipStream_t stream) {
+    hipLaunchKernelGGL((decode_kernel<KV, G>), dim3(a.splits, groups_y), dim3((64 * waves_for<KV, G>())), 0, stream, a);
+    return check_launch("decode_kernel");
 }
 
 template <int KV>
-int launch_split_g(const DecodeArgs& a, int G, int groups_y, hipStream_t stream) {
+int launch_g(const DecodeArgs& a, int G, int groups_y, hipStream_t stream) {
     switch (G) {
-        case 1: return launch_split<KV, 1>(a, groups_y, stream);
-        case 2: return launch_split<KV, 2>(a, groups_y, stream);
-        case 4: return launch_split<KV, 4>(a, groups_y, stream);
-        case 8: return launch_split<KV, 8>(a, groups_y, stream);
+        case 1: return launch<KV, 1>(a, groups_y, stream);
+        case 2: return launch<KV, 2>(a, groups_y, stream);
+        case 4: return launch<KV, 4>(a, groups_y, stream);
+        case 8: return launch<KV, 8>(a, groups_y, stream);
     }
     return set_error(BRASA_ERR_UNSUPPORTED, "decode: GQA group %d not compiled", G);
 }
 
+
 }  // namespace
 
-// Split plan: keys per split are a multiple of 128 (so splits <= ceil(lk / 128) and the
-// reference's partials size always suffices) chosen so that about 1024 workgroups cover the
-// 256 CUs. BRASA_DECODE_CHUNK overrides the chunk (a multiple of 128). The plan depends only
-// on (lk, workgroups per split), so results are reproducible bit for bit.
-void decode_plan(int lk, int wg_per_split, int* chunk_out, int* splits_out) {
-    static int env_chunk = [] {
-        const char* e = getenv("BRASA_DECODE_CHUNK");
-        int c = e ? atoi(e) : 0;
-        return (c > 0 && c % 128 == 0) ? c : 0;
+// Split plan. Keys per split are a multiple of `unit` = 32 keys x waves per workgroup (>= 128),
+// so there are at most
+// ceil(lk / 128) splits and the partials fit the reference's decode_partials_len(hq, lk)
+// floats. About BRASA_DECODE_WGS (default 256, one per CU) workgroups cover the GPU. The plan depends only on (lk, workgroups
+// per split), so results are reproducible bit for bit.
+void decode_plan(int lk, int wg_per_split, int unit, int* chunk_out, int* splits_out) {
+    static const int target_wgs = [] {
+        const char* e = getenv("BRASA_DECODE_WGS");
+        const int v = e ? atoi(e) : 0;
+        return v > 0 ? v : 256;
     }();
-    int chunk;
-    if (env_chunk) {
-        chunk = env_chunk;
-    } else {
-        const int max_splits = (lk + 127) / 128;
-        int target = (1024 + wg_per_split - 1) / wg_per_split;
-        if (target > max_splits) target = max_splits;
-        if (target < 1) target = 1;
-        chunk = ((lk + target - 1) / target + 127) / 128 * 128;
-    }
+    const int max_splits = (lk + 127) / 128;
+    int target = (target_wgs + wg_per_split - 1) / wg_per_split;
+    if (target > max_splits) target = max_splits;
+    if (target > kMaxSplits) target = kMaxSplits;
+    if (target < 1) target = 1;
+    const int chunk = ((lk + target - 1) / target + unit - 1) / unit * unit;
     *chunk_out = chunk;
     *splits_out = (lk + chunk - 1) / chunk;
 }
@@ -284,9 +561,9 @@ int decode_launch(const float* q, const void* k, const void* v, float* partials,
     a.q = q;
     a.k = static_cast<const uint8_t*>(k);
     a.v = static_cast<const uint8_t*>(v);
-    decode_plan(lk, groups_y, &a.chunk, &a.splits);
-    a.part_acc = partials;
-    a.part_ml = partials + (size_t)hq * a.splits * kDim;
+    const int waves = (kv == BRASA_KV_F16 && G <= 4) ? 8 : 4;  // waves_for<kv, G>
+    decode_plan(lk, groups_y, 32 * waves, &a.chunk, &a.splits);
+    a.part = partials;
     a.o = o;
     a.o_f16 = o_f16;
     a.hq = hq;
@@ -296,14 +573,14 @@ int decode_launch(const float* q, const void* k, const void* v, float* partials,
     a.scale = 1.0f / sqrtf(static_cast<float>(kDim));
     int st;
     switch (kv) {
-        case BRASA_KV_F32: st = launch_split_g<BRASA_KV_F32>(a, G, groups_y, stream); break;
-        case BRASA_KV_F16: st = launch_split_g<BRASA_KV_F16>(a, G, groups_y, stream); break;
-        case BRASA_KV_Q8_0: st = launch_split_g<BRASA_KV_Q8_0>(a, G, groups_y, stream); break;
+        case BRASA_KV_F32: st = launch_g<BRASA_KV_F32>(a, G, groups_y, stream); break;
+        case BRASA_KV_F16: st = launch_g<BRASA_KV_F16>(a, G, groups_y, stream); break;
+        case BRASA_KV_Q8_0: st = launch_g<BRASA_KV_Q8_0>(a, G, groups_y, stream); break;
         default: return set_error(BRASA_ERR_ARG, "decode: invalid kv type %d", kv);
     }
     if (st != BRASA_OK || a.splits == 1) return st;
-    hipLaunchKernelGGL(decode_reduce_kernel, dim3(hq), dim3(kDim), 0, stream, a.part_acc,
-                       a.part_ml, o, o_f16, a.splits);
+    hipLaunchKernelGGL(decode_reduce_kernel, dim3(hq, kDim / kRedSlice), dim3(64), 0,
+                       stream, partials, o, o_f16, hq, a.splits);
     return check_launch("decode_reduce_kernel");
 }
 

@@ -115,7 +115,7 @@ prefill_kernel(PrefillArgs a) {
             uint16_t hi[8], lo[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float sx = qvalid ? xs[j] * a.scale : 0.0f;
+                const float sx = qvalid ? as_f32(xs[j] * a.scale) : 0.0f;
                 if (QS) split_f16(sx, hi[j], lo[j]);
                 else hi[j] = f2h(sx);
             }
@@ -159,8 +159,8 @@ prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 if (KS) {
-                    split_f16(KV == BRASA_KV_Q8_0 ? kf[e] * ks : kf[e], khi[e], klo[e]);
-                    split_f16(KV == BRASA_KV_Q8_0 ? vf[e] * vs : vf[e], vhi[e], vlo[e]);
+                    split_f16(KV == BRASA_KV_Q8_0 ? as_f32(kf[e] * ks) : kf[e], khi[e], klo[e]);
+                    split_f16(KV == BRASA_KV_Q8_0 ? as_f32(vf[e] * vs) : vf[e], vhi[e], vlo[e]);
                 } else {
                     khi[e] = f2h(kf[e]);
                     vhi[e] = f2h(vf[e]);
@@ -275,8 +275,8 @@ prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int d = 32 * dt + 8 * g + 4 * u;
-            const float y0 = acc[dt][4 * g] * inv, y1 = acc[dt][4 * g + 1] * inv;
-            const float y2 = acc[dt][4 * g + 2] * inv, y3 = acc[dt][4 * g + 3] * inv;
+            const float y0 = as_f32(acc[dt][4 * g] * inv), y1 = as_f32(acc[dt][4 * g + 1] * inv);
+            const float y2 = as_f32(acc[dt][4 * g + 2] * inv), y3 = as_f32(acc[dt][4 * g + 3] * inv);
             if (OF32) {
                 *reinterpret_cast<float4*>(static_cast<float*>(a.o) + obase + d) =
                     make_float4(y0, y1, y2, y3);
