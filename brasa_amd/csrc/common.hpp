@@ -127,4 +127,29 @@ template <> struct Kv8<BRASA_KV_Q8_0> {
     __device__ __forceinline__ float scale() const { return h2f(sc); }
 };
 
+// 16-byte HBM -> LDS copy per lane (global_load_lds_dwordx4): lane i writes lds + 16 i.
+// M0 (the LDS base) is saved and restored around it. Issued as inline asm so that the compiler's vector-memory counter bookkeeping never relies on
+// it (its own waits can only become more conservative); the wait before the LDS reads of such
+// a tile is wait_vmcnt below.
+__device__ __forceinline__ void lds_dma16(const uint8_t* src, uint16_t* lds_wave_base) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)lds_wave_base);
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(src), "s"(m0)
+        : "memory");
+}
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited), then a compiler memory barrier.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+    asm volatile("" ::: "memory");
+}
+
 }  // namespace brasa

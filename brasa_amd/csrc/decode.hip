@@ -113,31 +113,6 @@ template <> struct Chunk<BRASA_KV_F32> {
     }
 };
 
-// 16-byte HBM -> LDS copy per lane (global_load_lds_dwordx4): lane i writes lds + 16 i.
-// M0 (the LDS base) is saved and restored around it. Issued as inline asm so that the compiler's vector-memory counter bookkeeping never relies on
-// it (its own waits can only become more conservative); the wait before the LDS reads of such
-// a tile is wait_vmcnt below.
-__device__ __forceinline__ void lds_dma16(const uint8_t* src, uint16_t* lds_wave_base) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)lds_wave_base);
-    uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %2\n\t"
-        "global_load_lds_dwordx4 %1, off\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(src), "s"(m0)
-        : "memory");
-}
-// s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited), then a compiler memory barrier.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-    asm volatile("" ::: "memory");
-}
-
 // Per-block register state of one wave: K fragments (2 key tiles x 4 dim steps), V chunks
 // (8 rows of 4 per lane), and for q8_0 the f16 scales of the rows each lane needs.
 template <int KV> struct Block {

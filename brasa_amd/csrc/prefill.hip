@@ -29,6 +29,8 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
 
 constexpr int kThreads = 256;
 constexpr int kTile = 64;       // keys per LDS tile
@@ -290,6 +292,199 @@ prefill_kernel(PrefillArgs a) {
     }
 }
 
+
+// ---- f16 cache, F16 / F16_PF32 precision: the hot path -------------------------------------
+//
+// Same work decomposition and MFMA formulation as prefill_kernel, with the K/V staging moved off
+// the vector ALUs: each 64-key stage is copied HBM -> LDS by global_load_lds_dwordx4 (raw f16
+// rows, 16-byte chunks XOR-swizzled so the operand reads are bank-conflict free), K A-operands
+// are ds_read_b128 of those rows and V^T A-operands are ds_read_tr16_b64 of the same row-major
+// tile. Two stages alternate so stage i + 1 streams in while stage i is contracted. The O
+// accumulator is only rescaled when a column's running max grows by more than 2^8 (P then stays
+// below 256, well inside f16), and masking runs only on tiles that cross the diagonal.
+constexpr int kStageHalves = kTile * kDim;  // one 64 x 128 f16 tile
+
+// physical 16-byte chunk of logical chunk c in row r
+__device__ __forceinline__ int kswz(int r, int c) { return c ^ (r & 15); }
+__device__ __forceinline__ int vswz(int r, int c) { return c ^ (4 * (r & 3)); }
+
+template <int HW, bool PS>
+__global__ void __launch_bounds__(kThreads, 2)
+prefill_f16_kernel(PrefillArgs a) {
+    constexpr int TPW = 32 * 4 / HW;
+    __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kStageHalves];
+    __shared__ __attribute__((aligned(16))) uint16_t s_vv[2][kStageHalves];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int col = lane & 31;
+    const int u = lane >> 5;
+
+    const int hg = blockIdx.x;
+    const int tile = a.ntiles - 1 - (int)blockIdx.y;
+    const int h = hg * HW + (wave % HW);
+    const int kh = (hg * HW) / a.group;
+    const int t0 = tile * TPW;
+    const int tw0 = t0 + 32 * (wave / HW);
+    const int lk = a.pos0 + a.tokens;
+    const int kend_wg = a.pos0 + min(t0 + TPW, a.tokens);
+    const int kend_w = a.pos0 + min(tw0 + 32, a.tokens);
+
+    const int tq = tw0 + col;
+    const bool qvalid = tq < a.tokens;
+    half8 qh[8];
+    {
+        const float* qrow = a.q + ((size_t)(qvalid ? tq : 0) * a.hq + h) * kDim;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float4* p = reinterpret_cast<const float4*>(qrow + 16 * t + 8 * u);
+            const float4 x0 = p[0], x1 = p[1];
+            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            uint16_t hi[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) hi[j] = f2h(qvalid ? as_f32(xs[j] * a.scale) : 0.0f);
+            qh[t] = pack8(hi);
+        }
+    }
+
+    f32x16 acc[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[dt][i] = 0.0f;
+    float m_used = -INFINITY;  // shift of the column's exponentials (log2 domain)
+    float lsum = 0.0f;
+    const int qabs = a.pos0 + tq;
+
+    // DMA of one stage: 16 K + 16 V instructions of 4 rows each; wave w issues rows 16 w .. +16
+    const size_t rstride = (size_t)a.hkv * 256;
+    const uint8_t* kbase = a.k + (size_t)kh * 256;
+    const uint8_t* vbase = a.v + (size_t)kh * 256;
+    const int lrow = lane >> 4, lchunk = lane & 15;
+    auto dma = [&](int kb, int buf) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 16 * wave + 4 * r + lrow;
+            const size_t g = (size_t)(kb + row) * rstride;
+            lds_dma16(kbase + g + 16 * kswz(row, lchunk), &s_k[buf][(16 * wave + 4 * r) * kDim]);
+            lds_dma16(vbase + g + 16 * vswz(row, lchunk), &s_vv[buf][(16 * wave + 4 * r) * kDim]);
+        }
+    };
+
+    dma(0, 0);
+    int buf = 0;
+    for (int kb = 0; kb < kend_wg; kb += kTile, buf ^= 1) {
+        __syncthreads();  // every wave is done with the other buffer
+        if (kb + kTile < kend_wg) {
+            dma(kb + kTile, buf ^ 1);
+            wait_vmcnt<8>();  // this stage's 8 copies landed (the next stage's 8 may fly)
+        } else {
+            wait_vmcnt<0>();
+        }
+        __syncthreads();  // ... for every wave
+        if (kb >= kend_w) continue;
+        const int nsub = (kb + 32 < kend_w) ? 2 : 1;
+        const uint16_t* kt = s_k[buf];
+        const uint16_t* vt = s_vv[buf];
+
+        f32x16 s[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[b][i] = 0.0f;
+            if (b < nsub) {
+                const int row = 32 * b + col;
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+                    s[b] = mfma(lds_b128(kt + row * kDim + 8 * kswz(row, 2 * t + u)), qh[t], s[b]);
+            }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int kb2 = kb + 32 * b;
+            const bool need_mask = (kb2 + 31 > a.pos0 + tw0) || (kb2 + 31 >= lk);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float x = s[b][i] * kLog2e;
+                if (b >= nsub) x = -INFINITY;
+                if (need_mask) {
+                    const int key = kb2 + 8 * (i / 4) + 4 * u + (i % 4);
+                    if (key > qabs || key >= lk) x = -INFINITY;
+                }
+                s[b][i] = x;
+                tmax = fmaxf(tmax, x);
+            }
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        // lazy rescale: only when the max exceeds the current shift by more than 8 (log2)
+        const bool grow = tmax > m_used + 8.0f;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+            const float alpha = grow ? __builtin_amdgcn_exp2f(m_used - tmax) : 1.0f;
+            if (grow) m_used = tmax;
+            lsum *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
+        }
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            if (b >= nsub) break;
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                uint16_t ph[8], pl[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float p = __builtin_amdgcn_exp2f(s[b][8 * st + j] - m_used);
+                    lsum += p;
+                    if (PS) split_f16(p, ph[j], pl[j]);
+                    else ph[j] = f2h(p);
+                }
+                const half8 pb = pack8(ph);
+                half8 plb;
+                if (PS) plb = pack8(pl);
+                // V^T A-operand: 16-lane group g = lane >> 4 covers dims 16 (g & 1) .. +16 and
+                // k-group u; tr16 source lane sl points at key (sl >> 2) of the 4, dims 4 (sl & 3)
+                const int sl = lane & 15;
+                const int key1 = 32 * b + 16 * st + 4 * u + (sl >> 2);
+                const int key2 = key1 + 8;
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) {
+                    const int c = 4 * dt + 2 * ((lane >> 4) & 1) + ((sl & 3) >> 1);
+                    const int o = 4 * (sl & 1);
+                    const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_v4s*)(vt + key1 * kDim + 8 * vswz(key1, c) + o));
+                    const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_v4s*)(vt + key2 * kDim + 8 * vswz(key2, c) + o));
+                    const half8 va = __builtin_bit_cast(
+                        half8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+                    acc[dt] = mfma(va, pb, acc[dt]);
+                    if (PS) acc[dt] = mfma(va, plb, acc[dt]);
+                }
+            }
+        }
+    }
+
+    const float L = lsum + __shfl_xor(lsum, 32, 64);
+    if (!qvalid) return;
+    const float inv = 1.0f / L;
+    const size_t obase = ((size_t)tq * a.hq + h) * kDim;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = 32 * dt + 8 * g + 4 * u;
+            uint2 w;
+            w.x = (uint32_t)f2h(as_f32(acc[dt][4 * g] * inv)) |
+                  ((uint32_t)f2h(as_f32(acc[dt][4 * g + 1] * inv)) << 16);
+            w.y = (uint32_t)f2h(as_f32(acc[dt][4 * g + 2] * inv)) |
+                  ((uint32_t)f2h(as_f32(acc[dt][4 * g + 3] * inv)) << 16);
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.o) + obase + d) = w;
+        }
+    }
+}
+
 template <int KV, int HW, bool QS, bool PS, bool OF32>
 int launch(const PrefillArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL((prefill_kernel<KV, HW, QS, PS, OF32>), dim3(a.hq / HW, a.ntiles),
@@ -297,8 +492,19 @@ int launch(const PrefillArgs& a, hipStream_t stream) {
     return check_launch("prefill_kernel");
 }
 
+template <int HW, bool PS>
+int launch_f16(const PrefillArgs& a, hipStream_t stream) {
+    hipLaunchKernelGGL((prefill_f16_kernel<HW, PS>), dim3(a.hq / HW, a.ntiles), dim3(kThreads), 0,
+                       stream, a);
+    return check_launch("prefill_f16_kernel");
+}
+
 template <int KV, int HW>
 int launch_prec(const PrefillArgs& a, int precision, hipStream_t stream) {
+    if constexpr (KV == BRASA_KV_F16) {
+        if (precision == BRASA_PREFILL_F16) return launch_f16<HW, false>(a, stream);
+        if (precision == BRASA_PREFILL_F16_PF32) return launch_f16<HW, true>(a, stream);
+    }
     switch (precision) {
         case BRASA_PREFILL_F32: return launch<KV, HW, true, true, true>(a, stream);
         case BRASA_PREFILL_F16_PF32: return launch<KV, HW, false, true, false>(a, stream);
