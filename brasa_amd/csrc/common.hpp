@@ -144,6 +144,24 @@ __device__ __forceinline__ void lds_dma16(const uint8_t* src, uint16_t* lds_wave
         : "v"(src), "s"(m0)
         : "memory");
 }
+// As lds_dma16 with a uniform 64-bit base in SGPRs and a per-lane 32-bit byte offset.
+__device__ __forceinline__ void lds_dma16_s(const uint8_t* sbase, uint32_t voff,
+                                            uint32_t lds_wave_base /* uniform LDS address */) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(voff), "s"(sbase), "s"(lds_wave_base)
+        : "memory");
+}
+// LDS address of a __shared__ location, as a 32-bit value.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
 // s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited), then a compiler memory barrier.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

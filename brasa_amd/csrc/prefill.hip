@@ -22,6 +22,8 @@
 //   * values that f16 cannot hold exactly (f32 and q8_0 caches, f32 Q, f32 P) are split as
 //     x = hi + lo with hi = f16(x), lo = f16(x - hi) and contracted with extra MFMAs
 //     (hi*hi + hi*lo + lo*hi), which keeps ~22 significant bits.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace brasa {
@@ -312,16 +314,22 @@ template <int HW, bool PS>
 __global__ void __launch_bounds__(kThreads, 2)
 prefill_f16_kernel(PrefillArgs a) {
     constexpr int TPW = 32 * 4 / HW;
+    constexpr int kTileBytes = kStageHalves * 2;
     __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kStageHalves];
     __shared__ __attribute__((aligned(16))) uint16_t s_vv[2][kStageHalves];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 31;
     const int u = lane >> 5;
 
+    // Work order: head groups fastest (they spread over the XCDs); query tiles heaviest first
+    // for the first half of the grid and lightest first for the second, so the two workgroups
+    // that share a CU (first and second wave of dispatch) carry about the same total work.
     const int hg = blockIdx.x;
-    const int tile = a.ntiles - 1 - (int)blockIdx.y;
+    const int half = (a.ntiles + 1) / 2;
+    const int y = (int)blockIdx.y;
+    const int tile = y < half ? a.ntiles - 1 - y : y - half;
     const int h = hg * HW + (wave % HW);
     const int kh = (hg * HW) / a.group;
     const int t0 = tile * TPW;
@@ -342,85 +350,97 @@ prefill_f16_kernel(PrefillArgs a) {
             const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
             uint16_t hi[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) hi[j] = f2h(qvalid ? as_f32(xs[j] * a.scale) : 0.0f);
+            for (int j = 0; j < 8; ++j) {
+                const float sx = as_f32(xs[j] * a.scale);  // f32 product, then f16
+                hi[j] = f2h(qvalid ? sx : 0.0f);
+            }
             qh[t] = pack8(hi);
         }
     }
+
+    // lane-constant byte offsets: K operand rows (per k-step t), V^T tr16 sources (per dt),
+    // DMA sources (per row quad r)
+    uint32_t koff[8], voff[4], kdo[4], vdo[4];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) koff[t] = col * 256 + 16 * kswz(col, 2 * t + u);
+    {
+        const int sl = lane & 15, j = sl >> 2;
+        const int low = 2 * ((lane >> 4) & 1) + ((sl & 3) >> 1);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+            voff[dt] = (4 * u + j) * 256 + 16 * (4 * (dt ^ j) + low) + 8 * (sl & 1);
+    }
+    const uint32_t rstride = (uint32_t)a.hkv * 256;
+    {
+        const int lrow = lane >> 4, lchunk = lane & 15;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 16 * wave + 4 * r + lrow;
+            kdo[r] = row * rstride + 16 * kswz(row, lchunk);
+            vdo[r] = row * rstride + 16 * vswz(row, lchunk);
+        }
+    }
+    const uint8_t* kbase = a.k + (size_t)kh * 256;
+    const uint8_t* vbase = a.v + (size_t)kh * 256;
+    const uint32_t lds_k = lds_addr(&s_k[0][0]) + wave * 16 * 256;
+    const uint32_t lds_v = lds_addr(&s_vv[0][0]) + wave * 16 * 256;
+    auto dma = [&](int kb, int buf) {
+        const uint8_t* kg = kbase + (size_t)kb * rstride;
+        const uint8_t* vg = vbase + (size_t)kb * rstride;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            lds_dma16_s(kg, kdo[r], lds_k + buf * kTileBytes + r * 1024);
+            lds_dma16_s(vg, vdo[r], lds_v + buf * kTileBytes + r * 1024);
+        }
+    };
 
     f32x16 acc[4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[dt][i] = 0.0f;
-    float m_used = -INFINITY;  // shift of the column's exponentials (log2 domain)
+    float m_used = -INFINITY;  // shift of the column's exponentials (raw score units)
     float lsum = 0.0f;
     const int qabs = a.pos0 + tq;
+    const float kGrow = 8.0f / kLog2e;  // rescale when the max grows by 2^8 in exp2 terms
 
-    // DMA of one stage: 16 K + 16 V instructions of 4 rows each; wave w issues rows 16 w .. +16
-    const size_t rstride = (size_t)a.hkv * 256;
-    const uint8_t* kbase = a.k + (size_t)kh * 256;
-    const uint8_t* vbase = a.v + (size_t)kh * 256;
-    const int lrow = lane >> 4, lchunk = lane & 15;
-    auto dma = [&](int kb, int buf) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = 16 * wave + 4 * r + lrow;
-            const size_t g = (size_t)(kb + row) * rstride;
-            lds_dma16(kbase + g + 16 * kswz(row, lchunk), &s_k[buf][(16 * wave + 4 * r) * kDim]);
-            lds_dma16(vbase + g + 16 * vswz(row, lchunk), &s_vv[buf][(16 * wave + 4 * r) * kDim]);
-        }
-    };
-
-    dma(0, 0);
-    int buf = 0;
-    for (int kb = 0; kb < kend_wg; kb += kTile, buf ^= 1) {
-        __syncthreads();  // every wave is done with the other buffer
-        if (kb + kTile < kend_wg) {
-            dma(kb + kTile, buf ^ 1);
-            wait_vmcnt<8>();  // this stage's 8 copies landed (the next stage's 8 may fly)
-        } else {
-            wait_vmcnt<0>();
-        }
-        __syncthreads();  // ... for every wave
-        if (kb >= kend_w) continue;
+    auto stage = [&](int kb, auto bufc) {
+        constexpr int buf = decltype(bufc)::value;
+        const uint8_t* kt = reinterpret_cast<const uint8_t*>(&s_k[buf][0]);
+        const uint8_t* vt = reinterpret_cast<const uint8_t*>(&s_vv[buf][0]);
         const int nsub = (kb + 32 < kend_w) ? 2 : 1;
-        const uint16_t* kt = s_k[buf];
-        const uint16_t* vt = s_vv[buf];
-
+        const f32x16 zero = {};
         f32x16 s[2];
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) s[b][i] = 0.0f;
             if (b < nsub) {
-                const int row = 32 * b + col;
+                s[b] = mfma(lds_b128(reinterpret_cast<const uint16_t*>(kt + koff[0] + b * 32 * 256)), qh[0], zero);
 #pragma unroll
-                for (int t = 0; t < 8; ++t)
-                    s[b] = mfma(lds_b128(kt + row * kDim + 8 * kswz(row, 2 * t + u)), qh[t], s[b]);
+                for (int t = 1; t < 8; ++t)
+                    s[b] = mfma(lds_b128(reinterpret_cast<const uint16_t*>(kt + koff[t] + b * 32 * 256)), qh[t], s[b]);
             }
         }
+        // causal mask (only on sub-blocks that reach past the wave's first query)
         float tmax = -INFINITY;
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-            const int kb2 = kb + 32 * b;
-            const bool need_mask = (kb2 + 31 > a.pos0 + tw0) || (kb2 + 31 >= lk);
+            if (b < nsub) {
+                const int kb2 = kb + 32 * b;
+                if ((kb2 + 31 > a.pos0 + tw0) || (kb2 + 31 >= lk)) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                float x = s[b][i] * kLog2e;
-                if (b >= nsub) x = -INFINITY;
-                if (need_mask) {
-                    const int key = kb2 + 8 * (i / 4) + 4 * u + (i % 4);
-                    if (key > qabs || key >= lk) x = -INFINITY;
+                    for (int i = 0; i < 16; ++i) {
+                        const int key = kb2 + 8 * (i / 4) + 4 * u + (i % 4);
+                        s[b][i] = (key > qabs || key >= lk) ? -INFINITY : s[b][i];
+                    }
                 }
-                s[b][i] = x;
-                tmax = fmaxf(tmax, x);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[b][i]);
             }
         }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        // lazy rescale: only when the max exceeds the current shift by more than 8 (log2)
-        const bool grow = tmax > m_used + 8.0f;
+        const bool grow = tmax > m_used + kGrow;
         if (__builtin_amdgcn_ballot_w64(grow)) {
-            const float alpha = grow ? __builtin_amdgcn_exp2f(m_used - tmax) : 1.0f;
+            const float alpha = grow ? __builtin_amdgcn_exp2f((m_used - tmax) * kLog2e) : 1.0f;
             if (grow) m_used = tmax;
             lsum *= alpha;
 #pragma unroll
@@ -428,6 +448,7 @@ prefill_f16_kernel(PrefillArgs a) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
         }
+        const float mb = m_used * kLog2e;
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             if (b >= nsub) break;
@@ -436,7 +457,7 @@ prefill_f16_kernel(PrefillArgs a) {
                 uint16_t ph[8], pl[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const float p = __builtin_amdgcn_exp2f(s[b][8 * st + j] - m_used);
+                    const float p = __builtin_amdgcn_exp2f(fmaf(s[b][8 * st + j], kLog2e, -mb));
                     lsum += p;
                     if (PS) split_f16(p, ph[j], pl[j]);
                     else ph[j] = f2h(p);
@@ -444,24 +465,40 @@ prefill_f16_kernel(PrefillArgs a) {
                 const half8 pb = pack8(ph);
                 half8 plb;
                 if (PS) plb = pack8(pl);
-                // V^T A-operand: 16-lane group g = lane >> 4 covers dims 16 (g & 1) .. +16 and
-                // k-group u; tr16 source lane sl points at key (sl >> 2) of the 4, dims 4 (sl & 3)
-                const int sl = lane & 15;
-                const int key1 = 32 * b + 16 * st + 4 * u + (sl >> 2);
-                const int key2 = key1 + 8;
+                const int rows = (32 * b + 16 * st) * 256;
 #pragma unroll
                 for (int dt = 0; dt < 4; ++dt) {
-                    const int c = 4 * dt + 2 * ((lane >> 4) & 1) + ((sl & 3) >> 1);
-                    const int o = 4 * (sl & 1);
                     const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (lds_v4s*)(vt + key1 * kDim + 8 * vswz(key1, c) + o));
+                        (lds_v4s*)(vt + voff[dt] + rows));
                     const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (lds_v4s*)(vt + key2 * kDim + 8 * vswz(key2, c) + o));
+                        (lds_v4s*)(vt + voff[dt] + rows + 8 * 256));
                     const half8 va = __builtin_bit_cast(
                         half8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
                     acc[dt] = mfma(va, pb, acc[dt]);
                     if (PS) acc[dt] = mfma(va, plb, acc[dt]);
                 }
+            }
+        }
+    };
+
+    // stages alternate between the two LDS buffers; stage i + 1 streams in during stage i
+    dma(0, 0);
+    for (int kb = 0; kb < kend_wg; kb += 2 * kTile) {
+#pragma unroll
+        for (int half_i = 0; half_i < 2; ++half_i) {
+            const int kbi = kb + half_i * kTile;
+            if (kbi >= kend_wg) break;
+            __syncthreads();  // every wave is done with the buffer the next copy overwrites
+            if (kbi + kTile < kend_wg) {
+                dma(kbi + kTile, half_i ^ 1);
+                wait_vmcnt<8>();
+            } else {
+                wait_vmcnt<0>();
+            }
+            __syncthreads();
+            if (kbi < kend_w) {
+                if (half_i == 0) stage(kbi, std::integral_constant<int, 0>{});
+                else stage(kbi, std::integral_constant<int, 1>{});
             }
         }
     }
