@@ -236,6 +236,33 @@ def load_traffic():
     return None
 
 
+COPY_BYTES = 256 << 20
+
+
+def profile_run(k: Kernels, stream: Stream, what: str) -> int:
+    """A short run for rocprofv3: three dispatches of a plain copy kernel of COPY_BYTES read and
+    COPY_BYTES written (store_kv with f32 cache type is a straight copy, the calibration of the
+    FETCH_SIZE / WRITE_SIZE counters), then the workload's kernels."""
+    n = COPY_BYTES // 4
+    src, dst = DeviceBuffer(COPY_BYTES), DeviceBuffer(COPY_BYTES)
+    fill_normal(src, n, 11, 1.0, stream)
+    for _ in range(3):
+        k.store_kv(KvType.F32, src, dst, n, stream)
+    stream.synchronize()
+    src.free()
+    dst.free()
+    if what == "decode":
+        layers = DecodeLayers(k, 16384, KvType.F16, stream)
+        for _ in range(3):
+            layers.step(stream)
+        stream.synchronize()
+        layers.free()
+    else:
+        bench_prefill(k, stream, 2048, 0, KvType.F16, 10, 2)
+    log(f"profile run '{what}' done")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -243,6 +270,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="only the headline decode + 2K prefill")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile", choices=("decode", "prefill"),
+                    help="short fixed run for rocprofv3 (kernel trace / counters), no JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the attention path has no "
@@ -251,6 +280,8 @@ def main() -> int:
     stream = Stream()
     k = Kernels(stream)
     log(f"device: {device_name()}")
+    if args.profile:
+        return profile_run(k, stream, args.profile)
 
     head, t_step = bench_decode(k, stream, 16384, KvType.F16, args.steps, args.warmup)
     pre2k, _ = bench_prefill(k, stream, 2048, 0, KvType.F16, max(args.steps, 20), args.warmup)
