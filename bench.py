@@ -26,7 +26,9 @@ sys.path.insert(0, ROOT)
 
 import numpy as np  # noqa: E402
 
-from brasa_amd import AttnShape, Kernels, KvType, OutDType, decode_partials_len  # noqa: E402
+from brasa_amd import (AttnShape, Kernels, KvType, OutDType, RopeTable,  # noqa: E402
+                       decode_batch_partials_len,
+                       decode_partials_len)  # noqa: E402
 from brasa_amd.device import (DeviceBuffer, Event, Stream, device_name, fill_normal,  # noqa: E402
                               synchronize)
 
@@ -141,8 +143,26 @@ def bench_ragged(k, stream, steps, warmup, seed=12345):
 
     t = time_steps(step, stream, steps, warmup)
     total = sum(decode_bytes(int(lk), KvType.F16) for lk in lens)
-    log(f"ragged decode x8: {t * 1e6:.1f} µs, {total / t / 1e9:.0f} GB/s")
-    return {"lengths": [int(x) for x in lens], "us": t * 1e6, "GBps": total / t / 1e9}
+    log(f"ragged decode x8, sequential calls: {t * 1e6:.1f} µs, {total / t / 1e9:.0f} GB/s")
+
+    # the same 8 sequences in one batched call
+    qb = DeviceBuffer(4 * 8 * HQ * DIM)
+    for i, (_, _, q, _, _, _) in enumerate(seqs):
+        synchronize()
+        qb.upload(q.download(np.float32), offset=4 * i * HQ * DIM)
+    ob = DeviceBuffer(4 * 8 * HQ * DIM)
+    pb = DeviceBuffer(4 * decode_batch_partials_len(HQ, lens))
+    ks, vs = [x[0] for x in seqs], [x[1] for x in seqs]
+    lks = [int(x) for x in lens]
+
+    def step_b(s):
+        k.decode_attention_batch(qb, ks, vs, lks, pb, ob, HQ, HKV, KvType.F16, OutDType.F32, s)
+
+    tb = time_steps(step_b, stream, steps, warmup)
+    log(f"ragged decode x8, one batched call: {tb * 1e6:.1f} µs, {total / tb / 1e9:.0f} GB/s")
+    return {"lengths": lks, "bytes": total, "us_sequential": t * 1e6,
+            "GBps_sequential": total / t / 1e9, "us_batched": tb * 1e6,
+            "GBps_batched": total / tb / 1e9}
 
 
 def bench_prefill(k, stream, tokens, pos0, kv, steps, warmup, seed=3):
@@ -168,6 +188,28 @@ def bench_prefill(k, stream, tokens, pos0, kv, steps, warmup, seed=3):
         b.free()
     return {"us": t * 1e6, "TFLOPs": tf, "flop": prefill_flops(tokens, pos0),
             "frac_mfma_f16_peak": tf / MFMA_F16_PEAK_TFLOPS}, t
+
+
+def bench_qkv(k, stream, tokens, kv, steps, warmup, seed=21):
+    """qk_norm_rope_store for `tokens` tokens at pos0 = 0 (the step before attention): bytes =
+    q, k, v read + q, k written (f32) + K and V cache rows written."""
+    nq, nk = tokens * HQ * DIM, tokens * HKV * DIM
+    bufs = [DeviceBuffer(4 * n) for n in (nq, nk, nk)]
+    for i, b in enumerate(bufs):
+        fill_normal(b, b.nbytes // 4, seed + i, 1.0, stream)
+    qn, kn = DeviceBuffer(4 * DIM), DeviceBuffer(4 * DIM)
+    fill_normal(qn, DIM, seed + 5, 1.0, stream)
+    fill_normal(kn, DIM, seed + 6, 1.0, stream)
+    kc, vc = DeviceBuffer(kv.bytes(nk)), DeviceBuffer(kv.bytes(nk))
+    table = RopeTable(1e6, DIM, max(tokens, 64))
+    shape = AttnShape(tokens, HQ, HKV, DIM, 0, kv)
+    stream.synchronize()
+    t = time_steps(lambda s: k.qk_norm_rope_store(kv, bufs, (qn, kn), 1e-6, table, (kc, vc),
+                                                  shape, s), stream, steps, warmup)
+    nbytes = 4 * (2 * nq + 3 * nk) + 2 * kv.bytes(nk)
+    log(f"qk_norm_rope_store kv={kv.name_str} T={tokens}: {t * 1e6:.2f} µs, "
+        f"{nbytes / t / 1e9:.0f} GB/s")
+    return {"us": t * 1e6, "bytes": nbytes, "GBps": nbytes / t / 1e9}
 
 
 def cpu_baseline(budget_s: float = 20.0):
@@ -293,6 +335,11 @@ def main() -> int:
         extra_decode["q8_16384"], _ = bench_decode(k, stream, 16384, KvType.Q8_0,
                                                    max(10, args.steps // 2), 2)
         extra_decode["ragged_8seq"] = bench_ragged(k, stream, max(10, args.steps // 2), 2)
+        extra_prefill["qk_norm_rope_store_f16_T1"] = bench_qkv(k, stream, 1, KvType.F16, 50, 5)
+        extra_prefill["qk_norm_rope_store_f16_T2048"] = bench_qkv(k, stream, 2048, KvType.F16,
+                                                                  20, 3)
+        extra_prefill["qk_norm_rope_store_q8_T2048"] = bench_qkv(k, stream, 2048, KvType.Q8_0,
+                                                                 20, 3)
         extra_prefill["T8192"], _ = bench_prefill(k, stream, 8192, 0, KvType.F16, 10, 2)
         extra_prefill["T512_pos16384"], _ = bench_prefill(k, stream, 512, 16384, KvType.F16, 10, 2)
     cpu = None if args.no_cpu else cpu_baseline()

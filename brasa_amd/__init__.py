@@ -7,10 +7,11 @@ plumbing the harnesses need.
 """
 from ._lib import BrasaError, LIB_PATH, build
 from .kernels import (DECODE_CHUNK, GQA_GROUPS, KV_ALIGN, AttnShape, Kernels, KvType, OutDType,
-                      PrefillPrecision, decode_partials_len, gqa_supported)
+                      PrefillPrecision, RopeTable, decode_batch_partials_len, decode_partials_len, gqa_supported,
+                      rope_table)
 
 __all__ = [
     "AttnShape", "BrasaError", "DECODE_CHUNK", "GQA_GROUPS", "KV_ALIGN", "Kernels", "KvType",
-    "LIB_PATH", "OutDType", "PrefillPrecision", "build", "decode_partials_len",
-    "gqa_supported",
+    "LIB_PATH", "OutDType", "PrefillPrecision", "RopeTable", "build", "decode_batch_partials_len", "decode_partials_len",
+    "gqa_supported", "rope_table",
 ]

@@ -25,6 +25,12 @@ class AttnShapeC(ctypes.Structure):
                 ("kv", INT)]
 
 
+class RopeTableC(ctypes.Structure):
+    """``brasa_rope_table_view`` (the device side of the reference's ``RopeTable``, lib.rs:1369-1374)."""
+
+    _fields_ = [("cos", VP), ("sin", VP), ("dim", SZ), ("max_pos", SZ)]
+
+
 # name -> (restype, argtypes) for every symbol the two public headers declare
 SYMBOLS = {
     "brasa_decode_partials_len": (SZ, [SZ, SZ]),
@@ -34,8 +40,16 @@ SYMBOLS = {
     "brasa_dequantize_kv_q8": (INT, [VP, VP, SZ, VP]),
     "brasa_decode_attention_lanes": (INT, [VP, VP, VP, VP, SZ, VP, INT, AttnShapeC, VP]),
     "brasa_decode_attention": (INT, [VP, VP, VP, VP, SZ, VP, INT, AttnShapeC, VP]),
+    "brasa_decode_batch_partials_len": (SZ, [SZ, VP, SZ]),
+    "brasa_decode_attention_batch": (INT, [VP, VP, VP, VP, SZ, VP, SZ, VP, INT, SZ, SZ, SZ, INT,
+                                           VP]),
     "brasa_flash_attention_with": (INT, [VP, VP, VP, VP, AttnShapeC, INT, VP]),
     "brasa_flash_attention": (INT, [VP, VP, VP, VP, AttnShapeC, VP]),
+    "brasa_rope_table": (INT, [ctypes.c_double, SZ, SZ, VP, VP]),
+    "brasa_rms_norm": (INT, [VP, VP, VP, SZ, SZ, ctypes.c_float, VP]),
+    "brasa_rope_neox": (INT, [VP, RopeTableC, SZ, SZ, SZ, SZ, VP]),
+    "brasa_qk_norm_rope_store": (INT, [INT, VP, VP, VP, VP, VP, ctypes.c_float, RopeTableC, VP,
+                                       VP, AttnShapeC, VP]),
     "brasa_last_error": (ctypes.c_char_p, []),
     "brasa_version": (ctypes.c_char_p, []),
     "brasa_rt_device_count": (INT, [ctypes.POINTER(INT)]),

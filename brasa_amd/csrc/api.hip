@@ -4,6 +4,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <vector>
 
 #include "../../include/brasa_hip_rt.h"
 #include "common.hpp"
@@ -16,6 +17,18 @@ int fill_u8_launch(void* dst, uint8_t value, size_t bytes, hipStream_t stream);
 int fill_normal_launch(float* out, size_t n, uint64_t seed, float scale, hipStream_t stream);
 int decode_launch(const float* q, const void* k, const void* v, float* partials, void* o,
                   int o_f16, int hq, int hkv, int lk, int kv, bool per_head, hipStream_t stream);
+int rms_norm_launch(const float* x, const float* w, float* out, size_t rows, size_t n, float eps,
+                    hipStream_t stream);
+int rope_neox_launch(float* x, const float* cos_t, const float* sin_t, size_t tokens,
+                     size_t heads, size_t dim, size_t pos0, hipStream_t stream);
+int qk_norm_rope_store_launch(int kv, float* q, float* k, const float* v, const float* qn,
+                              const float* kn, float eps, const float* cos_t, const float* sin_t,
+                              void* kdst, void* vdst, size_t tokens, size_t hq, size_t hkv,
+                              size_t pos0, hipStream_t stream);
+void rope_table_host(double theta, size_t dim, size_t max_pos, float* cos_out, float* sin_out);
+int decode_batch_launch(const float* q, const void* const* k, const void* const* v,
+                        const int* lk, int n, float* partials, void* o, int o_f16, int hq,
+                        int hkv, int kv, bool per_head, hipStream_t stream);
 int prefill_launch(const float* q, const void* k, const void* v, void* o, int tokens, int hq,
                    int hkv, int pos0, int kv, int precision, hipStream_t stream);
 
@@ -140,6 +153,45 @@ int brasa_decode_attention(const float* q, const void* k, const void* v, float* 
     return decode_common(q, k, v, partials, partials_len, o, o_dtype, shape, stream, true);
 }
 
+size_t brasa_decode_batch_partials_len(size_t hq, const size_t* lk, size_t n) {
+    size_t f = 0;
+    for (size_t i = 0; i < n; ++i) f += brasa_decode_partials_len(hq, lk[i]);
+    return f;
+}
+
+int brasa_decode_attention_batch(const float* q, const void* const* k, const void* const* v,
+                                 const size_t* lk, size_t n, float* partials,
+                                 size_t partials_len, void* o, int o_dtype, size_t hq,
+                                 size_t hkv, size_t dim, int kv, void* stream) {
+    g_err[0] = 0;
+    if (!valid_kv(kv)) return set_error(BRASA_ERR_ARG, "decode batch: invalid kv type %d", kv);
+    if (o_dtype != BRASA_OUT_F32 && o_dtype != BRASA_OUT_F16)
+        return set_error(BRASA_ERR_ARG, "decode batch: invalid output dtype %d", o_dtype);
+    if (dim != (size_t)kDim)
+        return set_error(BRASA_ERR_SHAPE, "decode_attention requires head_dim 128");
+    if (hkv == 0 || hq % hkv != 0) return set_error(BRASA_ERR_SHAPE, "hq must be a multiple of hkv");
+    if (!brasa_gqa_supported(hq, hkv))
+        return set_error(BRASA_ERR_UNSUPPORTED, "decode batch: GQA group %zu not compiled", hq / hkv);
+    if (hq > kMaxHeads || n > ((size_t)1 << 20))
+        return set_error(BRASA_ERR_SHAPE, "decode batch: shape too large");
+    if (n == 0) return BRASA_OK;
+    if (!lk || !k || !v) return set_error(BRASA_ERR_ARG, "decode batch: null array");
+    std::vector<int> lki(n);
+    for (size_t i = 0; i < n; ++i) {
+        if (lk[i] == 0) return set_error(BRASA_ERR_SHAPE, "decode batch: sequence %zu has no keys", i);
+        if (lk[i] > kMaxPositions) return set_error(BRASA_ERR_SHAPE, "decode batch: shape too large");
+        if (!k[i] || !v[i]) return set_error(BRASA_ERR_ARG, "decode batch: null cache pointer %zu", i);
+        lki[i] = (int)lk[i];
+    }
+    const size_t need = brasa_decode_batch_partials_len(hq, lk, n);
+    if (partials_len < need)
+        return set_error(BRASA_ERR_SCRATCH, "decode scratch too small (%zu < %zu floats)",
+                         partials_len, need);
+    if (!q || !partials || !o) return set_error(BRASA_ERR_ARG, "decode batch: null pointer");
+    return decode_batch_launch(q, k, v, lki.data(), (int)n, partials, o, o_dtype == BRASA_OUT_F16,
+                               (int)hq, (int)hkv, kv, false, as_stream(stream));
+}
+
 int brasa_flash_attention_with(const float* q, const void* k, const void* v, void* o,
                                brasa_attn_shape s, int precision, void* stream) {
     g_err[0] = 0;
@@ -163,6 +215,59 @@ int brasa_flash_attention_with(const float* q, const void* k, const void* v, voi
 int brasa_flash_attention(const float* q, const void* k, const void* v, void* o,
                           brasa_attn_shape shape, void* stream) {
     return brasa_flash_attention_with(q, k, v, o, shape, BRASA_PREFILL_F16, stream);
+}
+
+int brasa_rope_table(double theta, size_t dim, size_t max_pos, float* cos_out, float* sin_out) {
+    g_err[0] = 0;
+    if (dim == 0 || dim % 2 != 0) return set_error(BRASA_ERR_SHAPE, "rope_table: dim must be even");
+    if (max_pos > 0 && (!cos_out || !sin_out))
+        return set_error(BRASA_ERR_ARG, "rope_table: null pointer");
+    rope_table_host(theta, dim, max_pos, cos_out, sin_out);
+    return BRASA_OK;
+}
+
+int brasa_rms_norm(const float* x, const float* w, float* out, size_t rows, size_t n, float eps,
+                   void* stream) {
+    g_err[0] = 0;
+    if (rows == 0) return BRASA_OK;
+    if (n == 0 || n > ((size_t)1 << 24) || rows > ((size_t)1 << 30))
+        return set_error(BRASA_ERR_SHAPE, "rms_norm: bad row length %zu", n);
+    if (!x || !w || !out) return set_error(BRASA_ERR_ARG, "rms_norm: null pointer");
+    return rms_norm_launch(x, w, out, rows, n, eps, as_stream(stream));
+}
+
+int brasa_rope_neox(float* x, brasa_rope_table_view table, size_t tokens, size_t heads,
+                    size_t dim, size_t pos0, void* stream) {
+    g_err[0] = 0;
+    // lib.rs:579-583
+    if (dim != table.dim) return set_error(BRASA_ERR_SHAPE, "RoPE table dimension");
+    if (pos0 + tokens > table.max_pos) return set_error(BRASA_ERR_SHAPE, "position outside the RoPE table");
+    if (dim == 0 || dim % 2 != 0 || heads > kMaxHeads)
+        return set_error(BRASA_ERR_SHAPE, "rope_neox: bad shape");
+    if (tokens == 0 || heads == 0) return BRASA_OK;
+    if (!x || !table.cos || !table.sin) return set_error(BRASA_ERR_ARG, "rope_neox: null pointer");
+    return rope_neox_launch(x, table.cos, table.sin, tokens, heads, dim, pos0, as_stream(stream));
+}
+
+int brasa_qk_norm_rope_store(int kv, float* q, float* k, const float* v, const float* q_norm,
+                             const float* k_norm, float eps, brasa_rope_table_view table,
+                             void* k_dst, void* v_dst, brasa_attn_shape s, void* stream) {
+    g_err[0] = 0;
+    if (!valid_kv(kv)) return set_error(BRASA_ERR_ARG, "qk_norm_rope_store: invalid kv type %d", kv);
+    // lib.rs:996-1001
+    if (s.dim != (size_t)kDim)
+        return set_error(BRASA_ERR_SHAPE, "qk_norm_rope_store requires head_dim 128");
+    if (s.dim != table.dim) return set_error(BRASA_ERR_SHAPE, "RoPE table dimension");
+    if (s.pos0 + s.tokens > table.max_pos)
+        return set_error(BRASA_ERR_SHAPE, "position outside the RoPE table");
+    if (s.hq > kMaxHeads || s.hkv > kMaxHeads || s.tokens * (s.hq + 2 * s.hkv) > ((size_t)1 << 30))
+        return set_error(BRASA_ERR_SHAPE, "qk_norm_rope_store: shape too large");
+    if (s.tokens == 0) return BRASA_OK;
+    if (!q || !k || !v || !q_norm || !k_norm || !table.cos || !table.sin || !k_dst || !v_dst)
+        return set_error(BRASA_ERR_ARG, "qk_norm_rope_store: null pointer");
+    return qk_norm_rope_store_launch(kv, q, k, v, q_norm, k_norm, eps, table.cos, table.sin,
+                                     k_dst, v_dst, s.tokens, s.hq, s.hkv, s.pos0,
+                                     as_stream(stream));
 }
 
 const char* brasa_last_error(void) { return g_err; }

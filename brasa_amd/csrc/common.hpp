@@ -37,6 +37,16 @@ __device__ __forceinline__ float as_f32(float x) {
     return x;
 }
 
+// ---- q8_0 quantisation of one 32-group (quantize_kv_q8, crates/quant/src/qtype.rs:85-111) ----
+// d = f16(amax / 127) with an IEEE f32 divide rounded to nearest even in f16.
+__device__ __forceinline__ uint16_t q8_scale_bits(float amax) { return f2h(amax / 127.0f); }
+// q = d == 0 ? 0 : clamp(round_ties_even(x / d), -127, 127), as the int8 byte.
+__device__ __forceinline__ uint32_t q8_code(float x, float d) {
+    float qv = 0.0f;
+    if (d != 0.0f) qv = fminf(fmaxf(rintf(x / d), -127.0f), 127.0f);
+    return (uint32_t)(uint8_t)(int8_t)qv;
+}
+
 // ---- DPP / cross-lane helpers (wave64) ----------------------------------------------------
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {

@@ -23,6 +23,8 @@
 //   * q8_0: codes are exact in f16; K scales multiply the per-32-dim-group MFMA partials (one
 //     MFMA k-step is one group), V scales are folded into P per group; f32 caches are split
 //     hi + lo like Q.
+#include <cstring>
+
 #include "common.hpp"
 
 namespace brasa {
@@ -37,19 +39,40 @@ typedef __attribute__((address_space(3))) v4s lds_v4s;
 template <int KV, int G> constexpr int waves_for() { return (KV == BRASA_KV_F16 && G <= 4) ? 8 : 4; }
 constexpr int kBlock = 32;        // keys per wave iteration
 constexpr int kVStr = 144;        // V tile row stride in halves (256 B + 32 B pad)
-constexpr int kMaxSplits = 256;   // splits per call (their (m, l) sit in LDS during the merge)
+constexpr int kMaxSplits = 256;   // splits per sequence (the plan lengthens splits beyond that)
+
+// Sequences per launch: their descriptors travel in the kernel arguments (no device-side
+// metadata, so a call allocates and copies nothing).
+constexpr int kMaxSeqs = 64;
+
+struct SeqDesc {
+    const uint8_t* k;     // layer cache base of this sequence
+    const uint8_t* v;
+    size_t part_off;      // floats: this sequence's partials (acc [hq][splits][128], then ml)
+    int lk;               // keys
+    int splits;
+    int split0;           // first grid column of this sequence
+    int pad;
+};
 
 struct DecodeArgs {
-    const float* q;       // [hq, 128]
-    const uint8_t* k;     // layer cache base
-    const uint8_t* v;
-    float* part;          // caller scratch (arrival words, then partials)
-    void* o;              // [hq, 128]
+    const float* q;       // [nseq, hq, 128]
+    float* part;          // caller scratch
+    void* o;              // [nseq, hq, 128]
     int o_f16;
     int hq, hkv, group;   // group = hq / hkv
-    int lk, chunk, splits;
+    int chunk;            // keys per split (the same for every sequence)
+    int nseq;
     float scale;
+    SeqDesc seq[kMaxSeqs];
 };
+
+// Grid column -> sequence (uniform per workgroup; nseq is small).
+__device__ __forceinline__ int seq_of(const DecodeArgs& a, int col) {
+    int si = 0;
+    while (si + 1 < a.nseq && col >= a.seq[si + 1].split0) ++si;
+    return si;
+}
 
 __device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -63,8 +86,12 @@ __device__ __forceinline__ void split8(const float (&x)[8], half8& hi, half8& lo
     uint16_t hh[8], ll[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        hh[j] = f2h(x[j]);
-        ll[j] = f2h(x[j] - h2f(hh[j]));
+        // x must be one f32 value for both halves: the backend would otherwise fold a product
+        // x = a * b into a single-rounding f16 conversion for hi only, and when the f32 product
+        // lies exactly on an f16 tie, hi + lo then misses x by one f16 ulp.
+        const float xv = as_f32(x[j]);
+        hh[j] = f2h(xv);
+        ll[j] = f2h(xv - h2f(hh[j]));
     }
     h.x = pack2(hh[0], hh[1]); h.y = pack2(hh[2], hh[3]); h.z = pack2(hh[4], hh[5]); h.w = pack2(hh[6], hh[7]);
     l.x = pack2(ll[0], ll[1]); l.y = pack2(ll[2], ll[3]); l.z = pack2(ll[4], ll[5]); l.w = pack2(ll[6], ll[7]);
@@ -154,7 +181,10 @@ decode_kernel(DecodeArgs a) {
     __shared__ float s_m[kWaves][G];
     __shared__ float s_l[kWaves][G];
 
-    const int split = blockIdx.x;
+    const int si = seq_of(a, blockIdx.x);
+    const SeqDesc& sd = a.seq[si];
+    const int split = blockIdx.x - sd.split0;
+    const float* qseq = a.q + (size_t)si * a.hq * kDim;
     const int h0 = blockIdx.y * G;         // first query head of this workgroup
     const int kh = h0 / a.group;           // its KV head
     const int lane = threadIdx.x & 63;
@@ -169,7 +199,7 @@ decode_kernel(DecodeArgs a) {
     for (int t = 0; t < 4; ++t) {
         // unconditional 128-bit loads (a valid head for every lane), masked afterwards
         const f32x4* qp = reinterpret_cast<const f32x4*>(
-            a.q + (size_t)(h0 + (colq ? c16 : 0)) * kDim + 32 * t + 8 * u);
+            qseq + (size_t)(h0 + (colq ? c16 : 0)) * kDim + 32 * t + 8 * u);
         const f32x4 q0 = qp[0], q1 = qp[1];
         const float sc = colq ? a.scale : 0.0f;
         const float x[8] = {q0.x * sc, q0.y * sc, q0.z * sc, q0.w * sc,
@@ -178,10 +208,10 @@ decode_kernel(DecodeArgs a) {
     }
 
     const int s0 = split * a.chunk;
-    const int s1 = min(a.lk, s0 + a.chunk);
+    const int s1 = min(sd.lk, s0 + a.chunk);
     const size_t kstride = (size_t)a.hkv * RB;
-    const uint8_t* kbase = a.k + (size_t)kh * RB;
-    const uint8_t* vbase = a.v + (size_t)kh * RB;
+    const uint8_t* kbase = sd.k + (size_t)kh * RB;
+    const uint8_t* vbase = sd.v + (size_t)kh * RB;
     uint16_t* vt = &s_v[wave][0];
     uint16_t* vt2 = &s_v2[wave][0];
 
@@ -374,6 +404,10 @@ decode_kernel(DecodeArgs a) {
             jb += stride;
             if (jb >= s1) break;
         }
+        // The last prefetch's HBM -> LDS copies are still in flight. They must land before the
+        // wave ends: the workgroup's LDS is handed to the next workgroup on this CU when it
+        // exits, and a late copy would overwrite that workgroup's data.
+        if constexpr (DMA) wait_vmcnt<0>();
     }
 
     // ---- merge the wave's 4 k-groups (disjoint keys) and the 4 waves -----------------------
@@ -390,9 +424,11 @@ decode_kernel(DecodeArgs a) {
     }
     __syncthreads();
 
-    const bool multi = a.splits > 1;
-    float* acc_out = a.part;
-    float* ml_out = acc_out + (size_t)a.hq * a.splits * kDim;
+    const int splits = sd.splits;
+    const bool multi = splits > 1;
+    float* acc_out = a.part + sd.part_off;
+    float* ml_out = acc_out + (size_t)a.hq * splits * kDim;
+    const size_t obase = (size_t)si * a.hq * kDim;
     for (int idx = threadIdx.x; idx < G * kDim; idx += kThreads) {
         const int h = idx / kDim, d = idx % kDim;
         float M = s_m[0][h];
@@ -408,13 +444,13 @@ decode_kernel(DecodeArgs a) {
         const int hh = h0 + h;
         if (!multi) {
             const float out = A / L;
-            if (a.o_f16) reinterpret_cast<uint16_t*>(a.o)[hh * kDim + d] = f2h(out);
-            else reinterpret_cast<float*>(a.o)[hh * kDim + d] = out;
+            if (a.o_f16) reinterpret_cast<uint16_t*>(a.o)[obase + hh * kDim + d] = f2h(out);
+            else reinterpret_cast<float*>(a.o)[obase + hh * kDim + d] = out;
         } else {
-            acc_out[((size_t)hh * a.splits + split) * kDim + d] = A;
+            acc_out[((size_t)hh * splits + split) * kDim + d] = A;
             if (d == 0) {
-                ml_out[((size_t)hh * a.splits + split) * 2] = M;
-                ml_out[((size_t)hh * a.splits + split) * 2 + 1] = L;
+                ml_out[((size_t)hh * splits + split) * 2] = M;
+                ml_out[((size_t)hh * splits + split) * 2 + 1] = L;
             }
         }
     }
@@ -427,8 +463,22 @@ decode_kernel(DecodeArgs a) {
 constexpr int kRedSlice = 32;                          // dims per wave
 constexpr int kRedPer = 8;                             // splits per lane held in registers
 
-__global__ void __launch_bounds__(64)
-decode_reduce_kernel(const float* __restrict__ part, void* o, int o_f16, int hq, int splits) {
+struct ReduceArgs {
+    const float* part;
+    void* o;
+    int o_f16, hq, nseq;
+    int splits[kMaxSeqs];
+    size_t part_off[kMaxSeqs];
+};
+
+__global__ void __launch_bounds__(64) decode_reduce_kernel(ReduceArgs ra) {
+    const int si = blockIdx.z;
+    const int splits = ra.splits[si];
+    if (splits == 1) return;  // the split kernel wrote this sequence's output
+    const float* part = ra.part + ra.part_off[si];
+    const int hq = ra.hq, o_f16 = ra.o_f16;
+    void* o = o_f16 ? (void*)(static_cast<uint16_t*>(ra.o) + (size_t)si * hq * kDim)
+                    : (void*)(static_cast<float*>(ra.o) + (size_t)si * hq * kDim);
     const int h = blockIdx.x, d0 = blockIdx.y * kRedSlice;
     const int lane = threadIdx.x, oi = lane & 7, sub = lane >> 3;
     const f32x4* acc = reinterpret_cast<const f32x4*>(part + (size_t)h * splits * kDim + d0) + oi;
@@ -487,7 +537,8 @@ decode_reduce_kernel(const float* __restrict__ part, void* o, int o_f16, int hq,
 
 template <int KV, int G>
 int launch(const DecodeArgs& a, int groups_y, hipStream_t stream) {
-    hipLaunchKernelGGL((decode_kernel<KV, G>), dim3(a.splits, groups_y), dim3((64 * waves_for<KV, G>())), 0, stream, a);
+    const int cols = a.seq[a.nseq - 1].split0 + a.seq[a.nseq - 1].splits;
+    hipLaunchKernelGGL((decode_kernel<KV, G>), dim3(cols, groups_y), dim3((64 * waves_for<KV, G>())), 0, stream, a);
     return check_launch("decode_kernel");
 }
 
@@ -505,58 +556,108 @@ int launch_g(const DecodeArgs& a, int G, int groups_y, hipStream_t stream) {
 
 }  // namespace
 
-// Split plan. Keys per split are a multiple of `unit` = 32 keys x waves per workgroup (>= 128),
-// so there are at most
-// ceil(lk / 128) splits and the partials fit the reference's decode_partials_len(hq, lk)
-// floats. About BRASA_DECODE_WGS (default 256, one per CU) workgroups cover the GPU. The plan depends only on (lk, workgroups
-// per split), so results are reproducible bit for bit.
-void decode_plan(int lk, int wg_per_split, int unit, int* chunk_out, int* splits_out) {
+// Split plan for a batch of sequences: one split length `chunk` (a multiple of `unit` = 32 keys x
+// waves per workgroup, >= 128) for all of them, chosen so that about BRASA_DECODE_WGS (default
+// 256, one per CU) workgroups cover the GPU. A sequence of lk keys gets ceil(lk / chunk) <=
+// ceil(lk / 128) splits, so its partials fit the reference's decode_partials_len(hq, lk) floats.
+// The plan depends only on the lengths and the workgroups per split, so results are
+// reproducible bit for bit.
+int decode_chunk(const int* lk, int n, int wg_per_split, int unit) {
     static const int target_wgs = [] {
         const char* e = getenv("BRASA_DECODE_WGS");
         const int v = e ? atoi(e) : 0;
         return v > 0 ? v : 256;
     }();
-    const int max_splits = (lk + 127) / 128;
-    int target = (target_wgs + wg_per_split - 1) / wg_per_split;
-    if (target > max_splits) target = max_splits;
-    if (target > kMaxSplits) target = kMaxSplits;
+    long long total = 0;
+    for (int i = 0; i < n; ++i) total += lk[i];
+    long long target = (target_wgs + wg_per_split - 1) / wg_per_split;
     if (target < 1) target = 1;
-    const int chunk = ((lk + target - 1) / target + unit - 1) / unit * unit;
-    *chunk_out = chunk;
-    *splits_out = (lk + chunk - 1) / chunk;
+    long long chunk = (total + target - 1) / target;
+    chunk = (chunk + unit - 1) / unit * unit;
+    // at most kMaxSplits splits per sequence
+    for (int i = 0; i < n; ++i) {
+        const long long need = ((long long)lk[i] + kMaxSplits - 1) / kMaxSplits;
+        if (chunk < need) chunk = (need + unit - 1) / unit * unit;
+    }
+    return (int)chunk;
+}
+
+// Floats of scratch a batch uses (<= the sum of decode_partials_len over its sequences).
+size_t decode_batch_scratch(const int* lk, int n, int chunk, int hq) {
+    size_t f = 0;
+    for (int i = 0; i < n; ++i) f += (size_t)hq * ((lk[i] + chunk - 1) / chunk) * (kDim + 2);
+    return f;
+}
+
+int decode_batch_launch(const float* q, const void* const* k, const void* const* v,
+                        const int* lk, int n, float* partials, void* o, int o_f16, int hq,
+                        int hkv, int kv, bool per_head, hipStream_t stream) {
+    const int group = hq / hkv;
+    const int G = per_head ? 1 : group;
+    const int groups_y = per_head ? hq : hkv;
+    const int waves = (kv == BRASA_KV_F16 && G <= 4) ? 8 : 4;  // waves_for<kv, G>
+    const int chunk = decode_chunk(lk, n, groups_y, 32 * waves);
+    const size_t oelem = o_f16 ? 2 : 4;
+    size_t part_off = 0;
+    for (int b0 = 0; b0 < n; b0 += kMaxSeqs) {
+        const int nb = min(kMaxSeqs, n - b0);
+        DecodeArgs a;
+        memset(&a, 0, sizeof(a));
+        a.q = q + (size_t)b0 * hq * kDim;
+        a.part = partials;
+        a.o = static_cast<uint8_t*>(o) + (size_t)b0 * hq * kDim * oelem;
+        a.o_f16 = o_f16;
+        a.hq = hq;
+        a.hkv = hkv;
+        a.group = group;
+        a.chunk = chunk;
+        a.nseq = nb;
+        a.scale = 1.0f / sqrtf(static_cast<float>(kDim));
+        ReduceArgs ra;
+        memset(&ra, 0, sizeof(ra));
+        ra.part = partials;
+        ra.o = a.o;
+        ra.o_f16 = o_f16;
+        ra.hq = hq;
+        ra.nseq = nb;
+        int col = 0;
+        bool any_multi = false;
+        for (int i = 0; i < nb; ++i) {
+            SeqDesc& d = a.seq[i];
+            d.k = static_cast<const uint8_t*>(k[b0 + i]);
+            d.v = static_cast<const uint8_t*>(v[b0 + i]);
+            d.lk = lk[b0 + i];
+            d.splits = (d.lk + chunk - 1) / chunk;
+            d.split0 = col;
+            d.part_off = part_off;
+            col += d.splits;
+            part_off += (size_t)hq * d.splits * (kDim + 2);
+            ra.splits[i] = d.splits;
+            ra.part_off[i] = d.part_off;
+            any_multi |= d.splits > 1;
+        }
+        int st;
+        switch (kv) {
+            case BRASA_KV_F32: st = launch_g<BRASA_KV_F32>(a, G, groups_y, stream); break;
+            case BRASA_KV_F16: st = launch_g<BRASA_KV_F16>(a, G, groups_y, stream); break;
+            case BRASA_KV_Q8_0: st = launch_g<BRASA_KV_Q8_0>(a, G, groups_y, stream); break;
+            default: return set_error(BRASA_ERR_ARG, "decode: invalid kv type %d", kv);
+        }
+        if (st != BRASA_OK) return st;
+        if (!any_multi) continue;
+        hipLaunchKernelGGL(decode_reduce_kernel, dim3(hq, kDim / kRedSlice, nb), dim3(64), 0,
+                           stream, ra);
+        st = check_launch("decode_reduce_kernel");
+        if (st != BRASA_OK) return st;
+    }
+    return BRASA_OK;
 }
 
 int decode_launch(const float* q, const void* k, const void* v, float* partials, void* o,
                   int o_f16, int hq, int hkv, int lk, int kv, bool per_head,
                   hipStream_t stream) {
-    const int group = hq / hkv;
-    const int G = per_head ? 1 : group;
-    const int groups_y = per_head ? hq : hkv;
-    DecodeArgs a;
-    a.q = q;
-    a.k = static_cast<const uint8_t*>(k);
-    a.v = static_cast<const uint8_t*>(v);
-    const int waves = (kv == BRASA_KV_F16 && G <= 4) ? 8 : 4;  // waves_for<kv, G>
-    decode_plan(lk, groups_y, 32 * waves, &a.chunk, &a.splits);
-    a.part = partials;
-    a.o = o;
-    a.o_f16 = o_f16;
-    a.hq = hq;
-    a.hkv = hkv;
-    a.group = group;
-    a.lk = lk;
-    a.scale = 1.0f / sqrtf(static_cast<float>(kDim));
-    int st;
-    switch (kv) {
-        case BRASA_KV_F32: st = launch_g<BRASA_KV_F32>(a, G, groups_y, stream); break;
-        case BRASA_KV_F16: st = launch_g<BRASA_KV_F16>(a, G, groups_y, stream); break;
-        case BRASA_KV_Q8_0: st = launch_g<BRASA_KV_Q8_0>(a, G, groups_y, stream); break;
-        default: return set_error(BRASA_ERR_ARG, "decode: invalid kv type %d", kv);
-    }
-    if (st != BRASA_OK || a.splits == 1) return st;
-    hipLaunchKernelGGL(decode_reduce_kernel, dim3(hq, kDim / kRedSlice), dim3(64), 0,
-                       stream, partials, o, o_f16, hq, a.splits);
-    return check_launch("decode_reduce_kernel");
+    return decode_batch_launch(q, &k, &v, &lk, 1, partials, o, o_f16, hq, hkv, kv, per_head,
+                               stream);
 }
 
 }  // namespace brasa

@@ -56,16 +56,12 @@ __global__ void store_q8_kernel(const float* __restrict__ src, uint8_t* __restri
     amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
     amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
     if (grp >= groups) return;
-    const uint16_t dh = f2h(amax / 127.0f);
+    const uint16_t dh = q8_scale_bits(amax);
     const float d = h2f(dh);
     const float xs[4] = {x.x, x.y, x.z, x.w};
     uint32_t packed = 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        float qv = 0.0f;
-        if (d != 0.0f) qv = fminf(fmaxf(rintf(xs[e] / d), -127.0f), 127.0f);
-        packed |= ((uint32_t)(uint8_t)(int8_t)qv) << (8 * e);
-    }
+    for (int e = 0; e < 4; ++e) packed |= q8_code(xs[e], d) << (8 * e);
     uint8_t* row = dst + (grp >> 2) * kQ8Row;
     const int b = (int)(grp & 3);
     *reinterpret_cast<uint32_t*>(row + 32 * b + 4 * sub) = packed;

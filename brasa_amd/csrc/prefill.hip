@@ -50,7 +50,10 @@ struct PrefillArgs {
 };
 
 
+// x is materialised as one f32 value for both halves (see as_f32): a product folded into a
+// single-rounding conversion for hi alone would leave hi + lo one f16 ulp off at f16 ties.
 __device__ __forceinline__ void split_f16(float x, uint16_t& hi, uint16_t& lo) {
+    x = as_f32(x);
     hi = f2h(x);
     lo = f2h(x - h2f(hi));
 }

@@ -1,0 +1,223 @@
+// Producer side of the attention path on gfx950: per-head QK-RMSNorm, RoPE-NeoX and the KV-cache
+// write, fused in one launch, plus the unfused RMSNorm and RoPE it must agree with bit for bit.
+//
+// Behaviour follows Kernels::qk_norm_rope_store (crates/kernels/src/lib.rs:976-1025;
+// qkv.metal:37-94): for every token t and head, q and k rows are normalised
+// (x * (1 / sqrt(sum x^2 / 128 + eps))) * w, rotated by RoPE-NeoX at position pos0 + t with the
+// f64-computed cos/sin table, written back in place, and k (rotated) and v (as given) are stored
+// into the cache from pos0 on in the cache type (store_kv rounding: f16 RNE or q8_0).
+//
+// Design: one wave64 per 128-element row (lane l holds elements l and l + 64, which are exactly
+// a RoPE pair), four rows per workgroup. The sum of squares has one fixed order shared with the
+// unfused rms_norm kernel (lane partials in index order, then a xor butterfly 32, 16, .., 1), so
+// fused and unfused results are identical bits, as the reference's fused test demands
+// (crates/kernels/tests/fused.rs:8-98). The q8_0 groups of 32 are half-waves: the group amax is
+// five xor shuffles. HBM-bound: T * (hq + 2 hkv) * 512 B read, q/k rewritten, cache rows written.
+#include <cmath>
+#include <vector>
+
+#include "common.hpp"
+
+namespace brasa {
+namespace {
+
+constexpr int kRowsPerWg = 4;
+
+// Sum over the wave of the per-lane partials, in the fixed xor-butterfly order.
+__device__ __forceinline__ float wave_sum(float p) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) p += __shfl_xor(p, m, 64);
+    return p;
+}
+__device__ __forceinline__ float half_wave_max(float x) {
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m, 64));
+    return x;
+}
+// 1 / sqrt(ss / n + eps) with IEEE divides and square root (the reference's precise::sqrt).
+__device__ __forceinline__ float rms_scale(float ss, int n, float eps) {
+    return 1.0f / sqrtf(ss / (float)n + eps);
+}
+
+// rms_norm (lib.rs:531-547; norm.metal:8-48): one wave per row of n elements.
+__global__ void __launch_bounds__(64 * kRowsPerWg)
+rms_norm_kernel(const float* x, const float* __restrict__ w, float* out, int rows,
+                int n, float eps) {
+    const int row = blockIdx.x * kRowsPerWg + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* xr = x + (size_t)row * n;  // out may alias x (in-place use)
+    float p = 0.0f;
+    for (int i = lane; i < n; i += 64) p += xr[i] * xr[i];
+    const float scale = rms_scale(wave_sum(p), n, eps);
+    float* orow = out + (size_t)row * n;
+    for (int i = lane; i < n; i += 64) orow[i] = (xr[i] * scale) * w[i];
+}
+
+// rope_neox (lib.rs:569-596; rope.metal:8-27): one thread per pair (i, i + dim / 2).
+__global__ void rope_neox_kernel(float* x, const float* __restrict__ cos_t,
+                                 const float* __restrict__ sin_t, int tokens, int heads, int dim,
+                                 int pos0) {
+    const int half = dim / 2;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)tokens * heads * half) return;
+    const int i = (int)(idx % half);
+    const size_t th = idx / half;  // t * heads + h
+    const int t = (int)(th / heads);
+    float* v = x + th * dim;
+    const size_t p = (size_t)(pos0 + t) * half + i;
+    const float c = cos_t[p], s = sin_t[p];
+    const float a = v[i], b = v[i + half];
+    v[i] = a * c - b * s;
+    v[i + half] = b * c + a * s;
+}
+
+// Writes this lane's two elements (l and l + 64) of cache row `row`.
+template <int KV>
+__device__ __forceinline__ void store_row(uint8_t* cache, size_t row, int lane, float y0,
+                                          float y1) {
+    if constexpr (KV == BRASA_KV_F32) {
+        float* r = reinterpret_cast<float*>(cache) + row * kDim;
+        r[lane] = y0;
+        r[lane + 64] = y1;
+    } else if constexpr (KV == BRASA_KV_F16) {
+        uint16_t* r = reinterpret_cast<uint16_t*>(cache) + row * kDim;
+        r[lane] = f2h(y0);
+        r[lane + 64] = f2h(y1);
+    } else {
+        // groups: elements 32 g .. 32 g + 31; y0 is in group lane / 32, y1 in 2 + lane / 32
+        uint8_t* r = cache + row * kQ8Row;
+        const uint16_t d0 = q8_scale_bits(half_wave_max(fabsf(y0)));
+        const uint16_t d1 = q8_scale_bits(half_wave_max(fabsf(y1)));
+        r[lane] = (uint8_t)q8_code(y0, h2f(d0));
+        r[lane + 64] = (uint8_t)q8_code(y1, h2f(d1));
+        if ((lane & 31) == 0) {
+            uint16_t* sc = reinterpret_cast<uint16_t*>(r + 128);
+            sc[lane >> 5] = d0;
+            sc[2 + (lane >> 5)] = d1;
+        }
+    }
+}
+
+struct QkvArgs {
+    float* q;
+    float* k;
+    const float* v;
+    const float* qn;
+    const float* kn;
+    const float* cos_t;
+    const float* sin_t;
+    uint8_t* kc;
+    uint8_t* vc;
+    int hq, hkv, pos0, rows;
+    float eps;
+};
+
+// Row gr of T * (hq + 2 hkv): within a token, first the hq query heads, then the hkv key heads,
+// then the hkv value heads (the reference's order, qkv.metal:59-61).
+template <int KV>
+__global__ void __launch_bounds__(64 * kRowsPerWg) qk_norm_rope_store_kernel(QkvArgs a) {
+    const int gr = blockIdx.x * kRowsPerWg + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (gr >= a.rows) return;
+    const int per_tok = a.hq + 2 * a.hkv;
+    const int t = gr / per_tok, r = gr % per_tok;
+    if (r >= a.hq + a.hkv) {
+        const size_t vh = (size_t)t * a.hkv + (r - a.hq - a.hkv);
+        const float* vr = a.v + vh * kDim;
+        store_row<KV>(a.vc, vh, lane, vr[lane], vr[lane + 64]);
+        return;
+    }
+    const bool is_q = r < a.hq;
+    const size_t idx = is_q ? (size_t)t * a.hq + r : (size_t)t * a.hkv + (r - a.hq);
+    float* x = (is_q ? a.q : a.k) + idx * kDim;
+    const float* w = is_q ? a.qn : a.kn;
+    const float x0 = x[lane], x1 = x[lane + 64];
+    float p = 0.0f;
+    p += x0 * x0;
+    p += x1 * x1;
+    const float scale = rms_scale(wave_sum(p), kDim, a.eps);
+    const float a0 = (x0 * scale) * w[lane];
+    const float b0 = (x1 * scale) * w[lane + 64];
+    const size_t tp = (size_t)(a.pos0 + t) * (kDim / 2) + lane;
+    const float c = a.cos_t[tp], s = a.sin_t[tp];
+    const float y0 = a0 * c - b0 * s;
+    const float y1 = b0 * c + a0 * s;
+    x[lane] = y0;
+    x[lane + 64] = y1;
+    if (!is_q) store_row<KV>(a.kc, idx, lane, y0, y1);
+}
+
+unsigned row_blocks(size_t rows) { return (unsigned)((rows + kRowsPerWg - 1) / kRowsPerWg); }
+
+}  // namespace
+
+int rms_norm_launch(const float* x, const float* w, float* out, size_t rows, size_t n, float eps,
+                    hipStream_t stream) {
+    if (rows == 0) return BRASA_OK;
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(row_blocks(rows)), dim3(64 * kRowsPerWg), 0, stream,
+                       x, w, out, (int)rows, (int)n, eps);
+    return check_launch("rms_norm");
+}
+
+int rope_neox_launch(float* x, const float* cos_t, const float* sin_t, size_t tokens,
+                     size_t heads, size_t dim, size_t pos0, hipStream_t stream) {
+    const size_t pairs = tokens * heads * (dim / 2);
+    if (pairs == 0) return BRASA_OK;
+    hipLaunchKernelGGL(rope_neox_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0,
+                       stream, x, cos_t, sin_t, (int)tokens, (int)heads, (int)dim, (int)pos0);
+    return check_launch("rope_neox");
+}
+
+int qk_norm_rope_store_launch(int kv, float* q, float* k, const float* v, const float* qn,
+                              const float* kn, float eps, const float* cos_t, const float* sin_t,
+                              void* kdst, void* vdst, size_t tokens, size_t hq, size_t hkv,
+                              size_t pos0, hipStream_t stream) {
+    QkvArgs a;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.qn = qn;
+    a.kn = kn;
+    a.cos_t = cos_t;
+    a.sin_t = sin_t;
+    a.kc = static_cast<uint8_t*>(kdst);
+    a.vc = static_cast<uint8_t*>(vdst);
+    a.hq = (int)hq;
+    a.hkv = (int)hkv;
+    a.pos0 = (int)pos0;
+    a.rows = (int)(tokens * (hq + 2 * hkv));
+    a.eps = eps;
+    if (a.rows == 0) return BRASA_OK;
+    const dim3 grid(row_blocks(a.rows)), block(64 * kRowsPerWg);
+    switch (kv) {
+        case BRASA_KV_F32:
+            hipLaunchKernelGGL(qk_norm_rope_store_kernel<BRASA_KV_F32>, grid, block, 0, stream, a);
+            break;
+        case BRASA_KV_F16:
+            hipLaunchKernelGGL(qk_norm_rope_store_kernel<BRASA_KV_F16>, grid, block, 0, stream, a);
+            break;
+        case BRASA_KV_Q8_0:
+            hipLaunchKernelGGL(qk_norm_rope_store_kernel<BRASA_KV_Q8_0>, grid, block, 0, stream, a);
+            break;
+        default:
+            return set_error(BRASA_ERR_ARG, "qk_norm_rope_store: invalid kv type %d", kv);
+    }
+    return check_launch("qk_norm_rope_store");
+}
+
+// rope_table (lib.rs:1388-1404): cos/sin(p * theta^(-2 i / dim)) in f64, stored as f32.
+void rope_table_host(double theta, size_t dim, size_t max_pos, float* cos_out, float* sin_out) {
+    const size_t half = dim / 2;
+    std::vector<double> inv(half);
+    for (size_t i = 0; i < half; ++i) inv[i] = 1.0 / std::pow(theta, (double)(2 * i) / (double)dim);
+    for (size_t p = 0; p < max_pos; ++p) {
+        for (size_t i = 0; i < half; ++i) {
+            const double ang = (double)p * inv[i];
+            cos_out[p * half + i] = (float)std::cos(ang);
+            sin_out[p * half + i] = (float)std::sin(ang);
+        }
+    }
+}
+
+}  // namespace brasa

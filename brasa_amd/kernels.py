@@ -16,7 +16,7 @@ from __future__ import annotations
 import enum
 from dataclasses import dataclass
 
-from ._lib import AttnShapeC, check, lib
+from ._lib import AttnShapeC, RopeTableC, check, lib
 from .device import DeviceBuffer, Stream
 
 DECODE_CHUNK = 128
@@ -39,7 +39,7 @@ class KvType(enum.IntEnum):
     def bytes(self, n: int) -> int:
         if self is KvType.Q8_0:
             if n % KV_Q8_DIM:
-                from ._lib import BrasaError
+                from ._lib import RopeTableC, BrasaError
                 raise BrasaError(1, f"KV Q8: rows of {KV_Q8_DIM} values")
             return n // KV_Q8_DIM * KV_Q8_ROW
         return n * self.block_bytes() // 32
@@ -83,6 +83,11 @@ class AttnShape:
         return AttnShapeC(self.tokens, self.hq, self.hkv, self.dim, self.pos0, int(self.kv))
 
 
+def decode_batch_partials_len(hq: int, lks) -> int:
+    """Scratch floats of a batched decode: the sum of decode_partials_len over the sequences."""
+    return sum(decode_partials_len(hq, int(x)) for x in lks)
+
+
 def gqa_supported(hq: int, hkv: int) -> bool:
     return bool(lib().brasa_gqa_supported(hq, hkv))
 
@@ -106,6 +111,32 @@ def _stream(s) -> int | None:
     if s is None:
         return None
     return s.handle if isinstance(s, Stream) else int(s)
+
+
+def rope_table(theta: float, dim: int, max_pos: int):
+    """``rope_table`` (lib.rs:1388-1404) computed by the library on the host: (cos, sin) as f32
+    numpy arrays of shape [max_pos, dim // 2]."""
+    import numpy as np
+    half = dim // 2
+    cos = np.empty(max_pos * half, dtype=np.float32)
+    sin = np.empty(max_pos * half, dtype=np.float32)
+    check(lib().brasa_rope_table(float(theta), dim, max_pos, cos.ctypes.data, sin.ctypes.data))
+    return cos.reshape(max_pos, half), sin.reshape(max_pos, half)
+
+
+class RopeTable:
+    """``RopeTable::new`` (lib.rs:1376-1386): the f64-computed table uploaded to the device."""
+
+    def __init__(self, theta: float, dim: int, max_pos: int):
+        cos, sin = rope_table(theta, dim, max_pos)
+        self.cos = DeviceBuffer(max(cos.nbytes, 4))
+        self.sin = DeviceBuffer(max(sin.nbytes, 4))
+        self.cos.upload(cos)
+        self.sin.upload(sin)
+        self.dim, self.max_pos = dim, max_pos
+
+    def c(self) -> RopeTableC:
+        return RopeTableC(self.cos.ptr, self.sin.ptr, self.dim, self.max_pos)
 
 
 class Kernels:
@@ -143,6 +174,43 @@ class Kernels:
         check(lib().brasa_decode_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(partials), plen,
                                            _ptr(o), int(out), shape.c(),
                                            _stream(stream or self.stream)))
+
+    def decode_attention_batch(self, q, ks, vs, lks, partials: DeviceBuffer, o, hq: int,
+                               hkv: int, kv: KvType, out: OutDType = OutDType.F32, stream=None,
+                               partials_len: int | None = None) -> None:
+        """Ragged batched decode: sequence i has query q[i], caches ks[i] / vs[i] and lks[i]
+        keys; one launch for all of them (the reference decodes one sequence per call)."""
+        import ctypes
+        n = len(lks)
+        assert len(ks) == n and len(vs) == n
+        karr = (ctypes.c_void_p * max(n, 1))(*[_ptr(x) for x in ks])
+        varr = (ctypes.c_void_p * max(n, 1))(*[_ptr(x) for x in vs])
+        larr = (ctypes.c_size_t * max(n, 1))(*[int(x) for x in lks])
+        plen = partials.nbytes // 4 if partials_len is None else partials_len
+        check(lib().brasa_decode_attention_batch(
+            _ptr(q), ctypes.cast(karr, ctypes.c_void_p), ctypes.cast(varr, ctypes.c_void_p),
+            ctypes.cast(larr, ctypes.c_void_p), n, _ptr(partials), plen, _ptr(o), int(out), hq,
+            hkv, 128, int(kv), _stream(stream or self.stream)))
+
+    def rms_norm(self, x, w, out, rows: int, n: int, eps: float, stream=None) -> None:
+        check(lib().brasa_rms_norm(_ptr(x), _ptr(w), _ptr(out), rows, n, eps,
+                                   _stream(stream or self.stream)))
+
+    def rope_neox(self, x, table: RopeTable, tokens: int, heads: int, dim: int, pos0: int,
+                  stream=None) -> None:
+        check(lib().brasa_rope_neox(_ptr(x), table.c(), tokens, heads, dim, pos0,
+                                    _stream(stream or self.stream)))
+
+    def qk_norm_rope_store(self, kv: KvType, qkv, norms, eps: float, table: RopeTable, dst,
+                           shape: AttnShape, stream=None) -> None:
+        """``qk_norm_rope_store`` (lib.rs:976-1025): ``qkv = (q, k, v)``, ``norms = (qn, kn)``,
+        ``dst = (k_cache_at_pos0, v_cache_at_pos0)``."""
+        q, k, v = qkv
+        qn, kn = norms
+        kd, vd = dst
+        check(lib().brasa_qk_norm_rope_store(int(kv), _ptr(q), _ptr(k), _ptr(v), _ptr(qn),
+                                             _ptr(kn), eps, table.c(), _ptr(kd), _ptr(vd),
+                                             shape.c(), _stream(stream or self.stream)))
 
     def flash_attention(self, q, k, v, o, shape: AttnShape, stream=None) -> None:
         self.flash_attention_with(q, k, v, o, shape, PrefillPrecision.F16, stream)

@@ -123,6 +123,23 @@ int brasa_decode_attention(const float* q, const void* k, const void* v, float* 
                            void* stream);
 
 /*
+ * Ragged batched decode (no counterpart in the reference, which decodes one sequence per call,
+ * lib.rs:1110-1164; a caller batching sequences, e.g. a serving scheduler over session.rs:240-245,
+ * would otherwise issue one call per sequence). One launch of the split kernel (and one of the
+ * merge) covers n sequences: sequence i has one query q[i] (q: [n, hq, 128] f32), its own layer
+ * caches k[i] / v[i] (HOST arrays of device pointers, same layout as decode_attention_lanes) and
+ * lk[i] >= 1 keys (HOST array). o: [n, hq, 128] in o_dtype. Each sequence's result equals
+ * brasa_decode_attention_lanes on it alone. Scratch: partials_len >=
+ * brasa_decode_batch_partials_len(hq, lk, n) floats. Requires dim == 128 and a GQA group in
+ * {1, 2, 4, 8}.
+ */
+size_t brasa_decode_batch_partials_len(size_t hq, const size_t* lk, size_t n);
+int brasa_decode_attention_batch(const float* q, const void* const* k, const void* const* v,
+                                 const size_t* lk, size_t n, float* partials,
+                                 size_t partials_len, void* o, int o_dtype, size_t hq,
+                                 size_t hkv, size_t dim, int kv, void* stream);
+
+/*
  * Kernels::flash_attention_with (lib.rs:1185-1248; flash_attention.metal:152-323): causal GQA
  * prefill. q: [tokens, hq, 128] f32; query t (absolute position pos0 + t) attends to keys
  * [0, pos0 + t]. k/v: layer cache readable up to ceil64(pos0 + tokens) positions (values past
@@ -137,6 +154,53 @@ int brasa_flash_attention_with(const float* q, const void* k, const void* v, voi
 /* Kernels::flash_attention (lib.rs:1169-1180): brasa_flash_attention_with(.., F16). */
 int brasa_flash_attention(const float* q, const void* k, const void* v, void* o,
                           brasa_attn_shape shape, void* stream);
+
+/*
+ * RopeTable (lib.rs:1365-1386): device arrays cos/sin [max_pos, dim / 2] (f32) built from
+ * brasa_rope_table, plus their shape.
+ */
+typedef struct brasa_rope_table_view {
+    const float* cos;
+    const float* sin;
+    size_t dim;
+    size_t max_pos;
+} brasa_rope_table_view;
+
+/*
+ * rope_table (lib.rs:1388-1404), on the host: cos/sin(p * theta^(-2 i / dim)) for p < max_pos,
+ * i < dim / 2, computed in f64 and stored as f32 into HOST arrays of max_pos * dim / 2 floats
+ * (upload them once at load time, as RopeTable::new does).
+ */
+int brasa_rope_table(double theta, size_t dim, size_t max_pos, float* cos_out, float* sin_out);
+
+/*
+ * Kernels::rms_norm (lib.rs:529-547; norm.metal:8-48): out[r, :] = x[r, :] * (1 / sqrt(mean x^2
+ * + eps)) * w for rows of n values (f32); out may equal x. Same bits as the normalisation inside
+ * brasa_qk_norm_rope_store for n == 128.
+ */
+int brasa_rms_norm(const float* x, const float* w, float* out, size_t rows, size_t n, float eps,
+                   void* stream);
+
+/*
+ * Kernels::rope_neox (lib.rs:567-596; rope.metal:8-27): RoPE-NeoX in place on x [tokens, heads,
+ * dim] (f32) at positions pos0 .. pos0 + tokens. Requires dim == table.dim and
+ * pos0 + tokens <= table.max_pos.
+ */
+int brasa_rope_neox(float* x, brasa_rope_table_view table, size_t tokens, size_t heads,
+                    size_t dim, size_t pos0, void* stream);
+
+/*
+ * Kernels::qk_norm_rope_store (lib.rs:972-1025; qkv.metal:37-94), one launch: per token, q
+ * [tokens, hq, 128] and k [tokens, hkv, 128] (f32, updated in place) are RMS-normalised with
+ * q_norm / k_norm [128] and eps and rotated by RoPE-NeoX at pos0 + t; then k and v
+ * [tokens, hkv, 128] are stored into the caches k_dst / v_dst (pointing at row pos0 * hkv of
+ * the layer) in cache type `kv`, with store_kv's rounding. Bit-identical to brasa_rms_norm,
+ * brasa_rope_neox and brasa_store_kv in sequence. Requires dim == 128 == table.dim and
+ * pos0 + tokens <= table.max_pos (shape.kv is ignored; `kv` rules, as in the reference).
+ */
+int brasa_qk_norm_rope_store(int kv, float* q, float* k, const float* v, const float* q_norm,
+                             const float* k_norm, float eps, brasa_rope_table_view table,
+                             void* k_dst, void* v_dst, brasa_attn_shape shape, void* stream);
 
 /* Description of the last error on this thread ("" if none). */
 const char* brasa_last_error(void);

@@ -104,3 +104,79 @@ def test_prefill_and_store_asserts_without_device():
     # zero-size calls are no-ops
     k.store_kv(KvType.F16, fake, fake, 0)
     k.flash_attention(fake, fake, fake, fake, AttnShape(0, 32, 8, 128, 5, KvType.F16))
+
+
+class _FakeTable:
+    """A RoPE table view with fake device addresses (the calls below fail before any launch)."""
+
+    def __init__(self, dim, max_pos):
+        self.dim, self.max_pos = dim, max_pos
+
+    def c(self):
+        from brasa_amd._lib import RopeTableC
+        return RopeTableC(0x2000, 0x3000, self.dim, self.max_pos)
+
+
+def test_qkv_asserts_without_device():
+    k = Kernels()
+    fake = 0x1000
+    t = _FakeTable(128, 4096)
+    ok = AttnShape(5, 32, 8, 128, 37, KvType.F16)
+    qkv, norms, dst = (fake, fake, fake), (fake, fake), (fake, fake)
+    # lib.rs:996-1001: head_dim 128, table dimension, position inside the table
+    assert _err(lambda: k.qk_norm_rope_store(KvType.F16, qkv, norms, 1e-6, t, dst,
+                                             AttnShape(5, 32, 8, 64, 37, KvType.F16))) == 1
+    assert _err(lambda: k.qk_norm_rope_store(KvType.F16, qkv, norms, 1e-6, _FakeTable(64, 4096),
+                                             dst, ok)) == 1
+    assert _err(lambda: k.qk_norm_rope_store(KvType.F16, qkv, norms, 1e-6, _FakeTable(128, 41),
+                                             dst, ok)) == 1
+    assert _err(lambda: k.qk_norm_rope_store(7, qkv, norms, 1e-6, t, dst, ok)) == 5
+    assert _err(lambda: k.qk_norm_rope_store(KvType.F16, (fake, 0, fake), norms, 1e-6, t, dst,
+                                             ok)) == 5
+    # lib.rs:579-583
+    assert _err(lambda: k.rope_neox(fake, t, 16, 32, 128, 4081)) == 1
+    assert _err(lambda: k.rope_neox(fake, t, 16, 32, 64, 0)) == 1
+    assert _err(lambda: k.rms_norm(fake, fake, fake, 4, 0, 1e-6)) == 1
+    # zero-size calls are no-ops
+    k.qk_norm_rope_store(KvType.F16, qkv, norms, 1e-6, t, dst,
+                         AttnShape(0, 32, 8, 128, 37, KvType.F16))
+    k.rms_norm(fake, fake, fake, 0, 128, 1e-6)
+
+
+def test_rope_table_host_matches_oracle():
+    """brasa_rope_table runs on the host: same f32 bits as the oracle's f64 table
+    (lib.rs:1388-1404), including large positions."""
+    import numpy as np
+    import oracle
+    cos, sin = brasa_amd.rope_table(1e6, 128, 40960)
+    oc, os_ = oracle.rope_table(1e6, 128, 40960)
+    assert np.array_equal(cos.ravel().view(np.uint32), np.asarray(oc).view(np.uint32))
+    assert np.array_equal(sin.ravel().view(np.uint32), np.asarray(os_).view(np.uint32))
+    # position 0 is the identity; p * inv_freq for i = 0 is p radians
+    assert np.all(cos[0] == 1.0) and np.all(sin[0] == 0.0)
+    assert cos[1000, 0] == np.float32(np.cos(1000.0))
+
+
+def test_decode_batch_asserts_without_device():
+    k = Kernels()
+    fake = 0x1000
+
+    class Part:
+        ptr, nbytes = 0x1000, 4 << 20
+
+    lens = [100, 3000]
+    need = brasa_amd.decode_batch_partials_len(32, lens)
+    assert lib().brasa_decode_batch_partials_len(
+        32, (ctypes.c_size_t * 2)(*lens), 2) == need
+    # a sequence without keys, a bad group, a small scratch, head_dim != 128 is fixed at 128
+    assert _err(lambda: k.decode_attention_batch(fake, [fake, fake], [fake, fake], [0, 5], Part,
+                                                 fake, 32, 8, KvType.F16)) == 1
+    assert _err(lambda: k.decode_attention_batch(fake, [fake], [fake], [5], Part, fake, 24, 8,
+                                                 KvType.F16)) == 3
+    assert _err(lambda: k.decode_attention_batch(fake, [fake, fake], [fake, fake], lens, Part,
+                                                 fake, 32, 8, KvType.F16,
+                                                 partials_len=need - 1)) == 2
+    assert _err(lambda: k.decode_attention_batch(fake, [fake, 0], [fake, fake], lens, Part,
+                                                 fake, 32, 8, KvType.F16)) == 5
+    # an empty batch is a no-op
+    k.decode_attention_batch(fake, [], [], [], Part, fake, 32, 8, KvType.F16)
