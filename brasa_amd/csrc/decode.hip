@@ -36,8 +36,9 @@ typedef __attribute__((address_space(3))) v4s lds_v4s;
 
 // Waves per workgroup: f16 caches use 8 (2 per SIMD, so one computes while the other's loads
 // are in flight); the register-staged q8_0 / f32 paths use 4 (LDS).
-template <int KV, int G> constexpr int waves_for() { return (KV == BRASA_KV_F16 && G <= 4) ? 8 : 4; }
 constexpr int kBlock = 32;        // keys per wave iteration
+constexpr int kMaxWaves = 4;      // head groups per workgroup (one wave each)
+constexpr int kMinChunk = 128;    // keys per split >= DECODE_CHUNK keeps the scratch bound
 constexpr int kVStr = 144;        // V tile row stride in halves (256 B + 32 B pad)
 constexpr int kMaxSplits = 256;   // splits per sequence (the plan lengthens splits beyond that)
 
@@ -55,23 +56,30 @@ struct SeqDesc {
     int pad;
 };
 
+template <int NS>
 struct DecodeArgs {
     const float* q;       // [nseq, hq, 128]
     float* part;          // caller scratch
     void* o;              // [nseq, hq, 128]
     int o_f16;
     int hq, hkv, group;   // group = hq / hkv
+    int ngroups;          // head groups: hkv (one per KV head) or hq (one query head each)
     int chunk;            // keys per split (the same for every sequence)
     int nseq;
     float scale;
-    SeqDesc seq[kMaxSeqs];
+    SeqDesc seq[NS];      // NS = 1 for single-sequence calls (smaller kernel arguments)
 };
 
 // Grid column -> sequence (uniform per workgroup; nseq is small).
-__device__ __forceinline__ int seq_of(const DecodeArgs& a, int col) {
-    int si = 0;
-    while (si + 1 < a.nseq && col >= a.seq[si + 1].split0) ++si;
-    return si;
+template <int NS>
+__device__ __forceinline__ int seq_of(const DecodeArgs<NS>& a, int col) {
+    if constexpr (NS == 1) {
+        return 0;
+    } else {
+        int si = 0;
+        while (si + 1 < a.nseq && col >= a.seq[si + 1].split0) ++si;
+        return si;
+    }
 }
 
 __device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
@@ -86,10 +94,10 @@ __device__ __forceinline__ void split8(const float (&x)[8], half8& hi, half8& lo
     uint16_t hh[8], ll[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        // x must be one f32 value for both halves: the backend would otherwise fold a product
-        // x = a * b into a single-rounding f16 conversion for hi only, and when the f32 product
-        // lies exactly on an f16 tie, hi + lo then misses x by one f16 ulp.
-        const float xv = as_f32(x[j]);
+        // callers pass products through as_f32: the backend would otherwise fold x = a * b
+        // into a single-rounding f16 conversion for hi only, and when the f32 product lies
+        // exactly on an f16 tie, hi + lo then misses x by one f16 ulp
+        const float xv = x[j];
         hh[j] = f2h(xv);
         ll[j] = f2h(xv - h2f(hh[j]));
     }
@@ -158,15 +166,14 @@ __device__ __forceinline__ int q8_exp(uint16_t sc) {
     return e == 0 ? -14 : min(e - 15, 9);
 }
 
-template <int KV, int G>
-__global__ void __launch_bounds__((64 * waves_for<KV, G>()), 1)
-decode_kernel(DecodeArgs a) {
+template <int KV, int G, int NS>
+__global__ void __launch_bounds__(64 * kMaxWaves)
+decode_kernel(DecodeArgs<NS> a) {
     constexpr int RB = KvTraits<KV>::row_bytes;
     constexpr bool KS = Chunk<KV>::kSplit;
     constexpr bool Q8 = (KV == BRASA_KV_Q8_0);
     constexpr int NV = KS ? 2 : 1;
-    constexpr int kWaves = waves_for<KV, G>();
-    constexpr int kThreads = 64 * kWaves;
+    constexpr int kWaves = kMaxWaves;
     // f16 caches: V rows go HBM -> LDS directly (global_load_lds_dwordx4), double-buffered,
     // 16-byte chunks XOR-swizzled by 2 * (row & 3) so the transposed reads are conflict-free.
     // Other caches: V goes through registers (conversion), one padded tile (+ lo tile for f32).
@@ -177,18 +184,17 @@ decode_kernel(DecodeArgs a) {
     // second V buffer of the DMA path, a distinct object so the compiler can tell its loads
     // from the first buffer's when it places waits
     __shared__ __attribute__((aligned(16))) uint16_t s_v2[kWaves][DMA ? kBlock * kDim : 8];
-    __shared__ float s_acc[kWaves][G][kDim];
-    __shared__ float s_m[kWaves][G];
-    __shared__ float s_l[kWaves][G];
 
     const int si = seq_of(a, blockIdx.x);
     const SeqDesc& sd = a.seq[si];
     const int split = blockIdx.x - sd.split0;
     const float* qseq = a.q + (size_t)si * a.hq * kDim;
-    const int h0 = blockIdx.y * G;         // first query head of this workgroup
-    const int kh = h0 / a.group;           // its KV head
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
+    const int hg = blockIdx.y * (int)(blockDim.x >> 6) + wave;  // this wave's head group
+    if (hg >= a.ngroups) return;           // (no workgroup barrier follows)
+    const int h0 = hg * G;                 // its first query head
+    const int kh = h0 / a.group;           // its KV head
     const int c16 = lane & 15;             // MFMA row/column index
     const int u = lane >> 4;               // MFMA k-group (8 of the 32 k-slots)
     const bool colq = c16 < G;             // this lane's column is a query head
@@ -202,8 +208,9 @@ decode_kernel(DecodeArgs a) {
             qseq + (size_t)(h0 + (colq ? c16 : 0)) * kDim + 32 * t + 8 * u);
         const f32x4 q0 = qp[0], q1 = qp[1];
         const float sc = colq ? a.scale : 0.0f;
-        const float x[8] = {q0.x * sc, q0.y * sc, q0.z * sc, q0.w * sc,
-                            q1.x * sc, q1.y * sc, q1.z * sc, q1.w * sc};  // f32, as reference
+        const float x[8] = {as_f32(q0.x * sc), as_f32(q0.y * sc), as_f32(q0.z * sc),
+                            as_f32(q0.w * sc), as_f32(q1.x * sc), as_f32(q1.y * sc),
+                            as_f32(q1.z * sc), as_f32(q1.w * sc)};  // f32, as reference
         split8(x, qhi[t], qlo[t]);
     }
 
@@ -347,7 +354,7 @@ decode_kernel(DecodeArgs a) {
                 for (int j = 0; j < 8; ++j) {
                     const uint32_t w = (g < 2) ? b.vsc[j].x : b.vsc[j].y;
                     const uint16_t sc = (uint16_t)((g & 1) ? (w >> 16) : (w & 0xffffu));
-                    pg[j] = p[j] * __builtin_amdgcn_ldexpf(h2f(sc), -q8_exp(sc));
+                    pg[j] = as_f32(p[j] * __builtin_amdgcn_ldexpf(h2f(sc), -q8_exp(sc)));
                 }
                 split8(pg, phi[g], plo[g]);
             }
@@ -386,22 +393,21 @@ decode_kernel(DecodeArgs a) {
         }
     };
 
-    // ---- stream this wave's blocks: jb = s0 + 32 (wave + 4 n), next block's loads in flight --
-    const int stride = kWaves * kBlock;
-    int jb = s0 + wave * kBlock;
-    if (jb < s1) {
+    // ---- stream the split's 32-key blocks, the next block's loads in flight -----------------
+    int jb = s0;
+    {
         Block<KV> A, B;
         load(A, jb, 0);
         // the prefetch is unconditional (rows clamp to s1 - 1): a branch around it would make
         // the compiler wait for every outstanding load before the current block's V writes
         while (true) {
-            load(B, jb + stride, 1);
+            load(B, jb + kBlock, 1);
             compute(A, jb, 0);
-            jb += stride;
+            jb += kBlock;
             if (jb >= s1) break;
-            load(A, jb + stride, 0);
+            load(A, jb + kBlock, 0);
             compute(B, jb, 1);
-            jb += stride;
+            jb += kBlock;
             if (jb >= s1) break;
         }
         // The last prefetch's HBM -> LDS copies are still in flight. They must land before the
@@ -410,58 +416,49 @@ decode_kernel(DecodeArgs a) {
         if constexpr (DMA) wait_vmcnt<0>();
     }
 
-    // ---- merge the wave's 4 k-groups (disjoint keys) and the 4 waves -----------------------
+    // ---- this wave's partial for its G heads: combine the 4 k-groups' denominators ---------
     lsum += __shfl_xor(lsum, 16, 64);
     lsum += __shfl_xor(lsum, 32, 64);
-    if (colq) {
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-            *reinterpret_cast<f32x4*>(&s_acc[wave][c16][16 * dt + 4 * u]) = acc[dt];
-        if (u == 0) {
-            s_m[wave][c16] = m2[0];
-            s_l[wave][c16] = lsum;
-        }
-    }
-    __syncthreads();
-
+    if (!colq) return;
+    const int hh = h0 + c16;
     const int splits = sd.splits;
-    const bool multi = splits > 1;
-    float* acc_out = a.part + sd.part_off;
-    float* ml_out = acc_out + (size_t)a.hq * splits * kDim;
-    const size_t obase = (size_t)si * a.hq * kDim;
-    for (int idx = threadIdx.x; idx < G * kDim; idx += kThreads) {
-        const int h = idx / kDim, d = idx % kDim;
-        float M = s_m[0][h];
+    if (splits == 1) {
+        const float inv = 1.0f / lsum;
+        const size_t ob = ((size_t)si * a.hq + hh) * kDim;
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_m[w][h]);
-        float A = 0.0f, L = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float wt = __builtin_amdgcn_exp2f(s_m[w][h] - M);  // 0 for waves without keys
-            A = fmaf(s_acc[w][h][d], wt, A);
-            L = fmaf(s_l[w][h], wt, L);
-        }
-        const int hh = h0 + h;
-        if (!multi) {
-            const float out = A / L;
-            if (a.o_f16) reinterpret_cast<uint16_t*>(a.o)[obase + hh * kDim + d] = f2h(out);
-            else reinterpret_cast<float*>(a.o)[obase + hh * kDim + d] = out;
-        } else {
-            acc_out[((size_t)hh * splits + split) * kDim + d] = A;
-            if (d == 0) {
-                ml_out[((size_t)hh * splits + split) * 2] = M;
-                ml_out[((size_t)hh * splits + split) * 2 + 1] = L;
+        for (int dt = 0; dt < 8; ++dt) {
+            const int d = 16 * dt + 4 * u;
+            const f32x4 y = acc[dt] * inv;
+            if (a.o_f16) {
+                u32x2 w;
+                w.x = pack2(f2h(y.x), f2h(y.y));
+                w.y = pack2(f2h(y.z), f2h(y.w));
+                *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.o) + ob + d) = w;
+            } else {
+                *reinterpret_cast<f32x4*>(static_cast<float*>(a.o) + ob + d) = y;
             }
         }
+        return;
+    }
+    float* acc_out = a.part + sd.part_off + ((size_t)hh * splits + split) * kDim;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+        *reinterpret_cast<f32x4*>(acc_out + 16 * dt + 4 * u) = acc[dt];
+    if (u == 0) {
+        float* ml_out = a.part + sd.part_off + (size_t)a.hq * splits * kDim;
+        *reinterpret_cast<f32x2*>(ml_out + ((size_t)hh * splits + split) * 2) = f32x2{m2[0], lsum};
     }
 }
 
-// Second pass (attn_decode_reduce, decode_attention.metal:68-84): one wave per (head, 32-dim
-// slice). Lane = (split subset sub = lane / 8, float4 column oi = lane % 8): every lane issues
-// all its loads at once ((m, l) and the acc float4 of splits sub, sub + 8, ...), so the pass
-// costs one memory round trip; max, denominator and the split sum are xor-shuffle reductions.
-constexpr int kRedSlice = 32;                          // dims per wave
-constexpr int kRedPer = 8;                             // splits per lane held in registers
+// Second pass (attn_decode_reduce, decode_attention.metal:68-84): one workgroup of 4 waves per
+// (head, 16-dim slice). Thread t owns float4 column t % 4 of the slice and splits t / 4 + 64 r;
+// it loads all of them at once and folds them with the running-max form of the split merge, so
+// the pass costs one memory round trip for up to 128 splits. The 64 split lanes are then merged
+// by xor shuffles and, across the 4 waves, through LDS, always in the same order.
+constexpr int kRedSlice = 16;                           // dims per workgroup
+constexpr int kRedThreads = 256;
+constexpr int kRedLanes = kRedThreads / (kRedSlice / 4);  // 64 split lanes
+constexpr int kRedPer = 2;                              // splits per lane per round
 
 struct ReduceArgs {
     const float* part;
@@ -471,122 +468,157 @@ struct ReduceArgs {
     size_t part_off[kMaxSeqs];
 };
 
-__global__ void __launch_bounds__(64) decode_reduce_kernel(ReduceArgs ra) {
+// (M, A, L) <- merge of (M, A, L) and (m, a, l): M = max, weights 2^(m - M) (0 for an empty side)
+__device__ __forceinline__ void merge_split(float& M, f32x4& A, float& L, float m, f32x4 a,
+                                            float l) {
+    const float Mn = fmaxf(M, m);
+    const float w0 = (M == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(M - Mn);
+    const float w1 = (m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - Mn);
+    A = A * w0 + a * w1;
+    L = L * w0 + l * w1;
+    M = Mn;
+}
+
+__global__ void __launch_bounds__(kRedThreads) decode_reduce_kernel(ReduceArgs ra) {
     const int si = blockIdx.z;
     const int splits = ra.splits[si];
     if (splits == 1) return;  // the split kernel wrote this sequence's output
     const float* part = ra.part + ra.part_off[si];
     const int hq = ra.hq, o_f16 = ra.o_f16;
-    void* o = o_f16 ? (void*)(static_cast<uint16_t*>(ra.o) + (size_t)si * hq * kDim)
-                    : (void*)(static_cast<float*>(ra.o) + (size_t)si * hq * kDim);
     const int h = blockIdx.x, d0 = blockIdx.y * kRedSlice;
-    const int lane = threadIdx.x, oi = lane & 7, sub = lane >> 3;
+    const int t = threadIdx.x, oi = t & 3, sub = t >> 2;
+    const int lane = t & 63, wave = t >> 6;
     const f32x4* acc = reinterpret_cast<const f32x4*>(part + (size_t)h * splits * kDim + d0) + oi;
     const f32x2* ml = reinterpret_cast<const f32x2*>(part + (size_t)hq * splits * kDim) + (size_t)h * splits;
-    float M = -INFINITY;
-    for (int s0 = sub; s0 < splits; s0 += 8 * kRedPer) {  // max pass over (m, l) (tiny)
-#pragma unroll
-        for (int r = 0; r < kRedPer; ++r) {
-            const int s = s0 + 8 * r;
-            if (s < splits) M = fmaxf(M, ml[s].x);
-        }
-    }
-#pragma unroll
-    for (int x = 8; x <= 32; x <<= 1) M = fmaxf(M, __shfl_xor(M, x, 64));
+    float M = -INFINITY, L = 0.0f;
     f32x4 A = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    float L = 0.0f;
-    for (int s0 = sub; s0 < splits; s0 += 8 * kRedPer) {
+    for (int s0 = sub; s0 < splits; s0 += kRedLanes * kRedPer) {
         f32x2 mlv[kRedPer];
         f32x4 av[kRedPer];
 #pragma unroll
         for (int r = 0; r < kRedPer; ++r) {
-            const int s = min(s0 + 8 * r, splits - 1);
+            const int s = min(s0 + kRedLanes * r, splits - 1);
             mlv[r] = ml[s];
             av[r] = acc[(size_t)s * (kDim / 4)];
         }
 #pragma unroll
-        for (int r = 0; r < kRedPer; ++r) {
-            if (s0 + 8 * r < splits) {
-                const float w = __builtin_amdgcn_exp2f(mlv[r].x - M);
-                A += av[r] * w;
-                L = fmaf(mlv[r].y, w, L);
-            }
-        }
+        for (int r = 0; r < kRedPer; ++r)
+            if (s0 + kRedLanes * r < splits) merge_split(M, A, L, mlv[r].x, av[r], mlv[r].y);
     }
+    // lanes with the same column: xor 4, 8, 16, 32
 #pragma unroll
-    for (int x = 8; x <= 32; x <<= 1) {
-        L += __shfl_xor(L, x, 64);
-        A.x += __shfl_xor(A.x, x, 64);
-        A.y += __shfl_xor(A.y, x, 64);
-        A.z += __shfl_xor(A.z, x, 64);
-        A.w += __shfl_xor(A.w, x, 64);
+    for (int x = 4; x <= 32; x <<= 1) {
+        const f32x4 a = f32x4{__shfl_xor(A.x, x, 64), __shfl_xor(A.y, x, 64),
+                              __shfl_xor(A.z, x, 64), __shfl_xor(A.w, x, 64)};
+        merge_split(M, A, L, __shfl_xor(M, x, 64), a, __shfl_xor(L, x, 64));
     }
-    if (sub == 0) {
-        const float y[4] = {A.x / L, A.y / L, A.z / L, A.w / L};
-        const int off = h * kDim + d0 + 4 * oi;
-        if (o_f16) {
-            uint2 w;
-            w.x = pack2(f2h(y[0]), f2h(y[1]));
-            w.y = pack2(f2h(y[2]), f2h(y[3]));
-            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(o) + off) = w;
-        } else {
-            *reinterpret_cast<f32x4*>(static_cast<float*>(o) + off) = f32x4{y[0], y[1], y[2], y[3]};
-        }
+    __shared__ f32x4 s_a[4][4];
+    __shared__ float s_m[4][4], s_l[4][4];
+    if (lane < 4) {
+        s_a[wave][lane] = A;
+        s_m[wave][lane] = M;
+        s_l[wave][lane] = L;
+    }
+    __syncthreads();
+    if (t >= 4) return;
+    M = s_m[0][t];
+    A = s_a[0][t];
+    L = s_l[0][t];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) merge_split(M, A, L, s_m[w][t], s_a[w][t], s_l[w][t]);
+    const f32x4 y = A / L;
+    const size_t off = ((size_t)si * hq + h) * kDim + d0 + 4 * oi;
+    if (o_f16) {
+        u32x2 w;
+        w.x = pack2(f2h(y.x), f2h(y.y));
+        w.y = pack2(f2h(y.z), f2h(y.w));
+        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(ra.o) + off) = w;
+    } else {
+        *reinterpret_cast<f32x4*>(static_cast<float*>(ra.o) + off) = y;
     }
 }
 
-template <int KV, int G>
-int launch(const DecodeArgs& a, int groups_y, hipStream_t stream) {
+template <int KV, int G, int NS>
+int launch(const DecodeArgs<NS>& a, int waves, hipStream_t stream) {
     const int cols = a.seq[a.nseq - 1].split0 + a.seq[a.nseq - 1].splits;
-    hipLaunchKernelGGL((decode_kernel<KV, G>), dim3(cols, groups_y), dim3((64 * waves_for<KV, G>())), 0, stream, a);
+    const int rows = (a.ngroups + waves - 1) / waves;
+    hipLaunchKernelGGL((decode_kernel<KV, G, NS>), dim3(cols, rows), dim3(64 * waves), 0, stream, a);
     return check_launch("decode_kernel");
 }
 
-template <int KV>
-int launch_g(const DecodeArgs& a, int G, int groups_y, hipStream_t stream) {
+template <int KV, int NS>
+int launch_g(const DecodeArgs<NS>& a, int G, int waves, hipStream_t stream) {
     switch (G) {
-        case 1: return launch<KV, 1>(a, groups_y, stream);
-        case 2: return launch<KV, 2>(a, groups_y, stream);
-        case 4: return launch<KV, 4>(a, groups_y, stream);
-        case 8: return launch<KV, 8>(a, groups_y, stream);
+        case 1: return launch<KV, 1, NS>(a, waves, stream);
+        case 2: return launch<KV, 2, NS>(a, waves, stream);
+        case 4: return launch<KV, 4, NS>(a, waves, stream);
+        case 8: return launch<KV, 8, NS>(a, waves, stream);
     }
     return set_error(BRASA_ERR_UNSUPPORTED, "decode: GQA group %d not compiled", G);
 }
 
 
+template <int NS>
+int launch_kv(const DecodeArgs<NS>& a, int kv, int G, int waves, hipStream_t stream) {
+    switch (kv) {
+        case BRASA_KV_F32: return launch_g<BRASA_KV_F32>(a, G, waves, stream);
+        case BRASA_KV_F16: return launch_g<BRASA_KV_F16>(a, G, waves, stream);
+        case BRASA_KV_Q8_0: return launch_g<BRASA_KV_Q8_0>(a, G, waves, stream);
+    }
+    return set_error(BRASA_ERR_ARG, "decode: invalid kv type %d", kv);
+}
+
+// The first sequence of `a` as single-sequence arguments.
+DecodeArgs<1> one_seq(const DecodeArgs<kMaxSeqs>& a) {
+    DecodeArgs<1> b;
+    b.q = a.q;
+    b.part = a.part;
+    b.o = a.o;
+    b.o_f16 = a.o_f16;
+    b.hq = a.hq;
+    b.hkv = a.hkv;
+    b.group = a.group;
+    b.ngroups = a.ngroups;
+    b.chunk = a.chunk;
+    b.nseq = 1;
+    b.scale = a.scale;
+    b.seq[0] = a.seq[0];
+    return b;
+}
+
 }  // namespace
 
-// Split plan for a batch of sequences: one split length `chunk` (a multiple of `unit` = 32 keys x
-// waves per workgroup, >= 128) for all of them, chosen so that about BRASA_DECODE_WGS (default
-// 256, one per CU) workgroups cover the GPU. A sequence of lk keys gets ceil(lk / chunk) <=
-// ceil(lk / 128) splits, so its partials fit the reference's decode_partials_len(hq, lk) floats.
-// The plan depends only on the lengths and the workgroups per split, so results are
-// reproducible bit for bit.
-int decode_chunk(const int* lk, int n, int wg_per_split, int unit) {
+// Launch plan for a batch of sequences: one split length `chunk` (a multiple of 32 keys and at
+// least 128, so a sequence of lk keys has at most ceil(lk / 128) splits and its partials fit the
+// reference's decode_partials_len(hq, lk) floats), and `waves` head groups per workgroup (4, 2
+// or 1: the most that still gives about BRASA_DECODE_WGS workgroups, default 256 = one per CU).
+// The plan depends only on the lengths and head counts, so results are reproducible bit for bit.
+void decode_plan(const int* lk, int n, int ngroups, int* chunk_out, int* waves_out) {
     static const int target_wgs = [] {
         const char* e = getenv("BRASA_DECODE_WGS");
         const int v = e ? atoi(e) : 0;
         return v > 0 ? v : 256;
     }();
-    long long total = 0;
-    for (int i = 0; i < n; ++i) total += lk[i];
-    long long target = (target_wgs + wg_per_split - 1) / wg_per_split;
-    if (target < 1) target = 1;
-    long long chunk = (total + target - 1) / target;
-    chunk = (chunk + unit - 1) / unit * unit;
+    long long total = 0, max_splits = 0;
+    for (int i = 0; i < n; ++i) {
+        total += lk[i];
+        max_splits += (lk[i] + kMinChunk - 1) / kMinChunk;
+    }
+    int waves = kMaxWaves;
+    while (waves > 1 && max_splits * ((ngroups + waves - 1) / waves) < target_wgs) waves >>= 1;
+    const long long rows = (ngroups + waves - 1) / waves;
+    long long splits = (target_wgs + rows - 1) / rows;
+    if (splits < 1) splits = 1;
+    long long chunk = (total + splits - 1) / splits;
+    chunk = (chunk + kBlock - 1) / kBlock * kBlock;
+    if (chunk < kMinChunk) chunk = kMinChunk;
     // at most kMaxSplits splits per sequence
     for (int i = 0; i < n; ++i) {
         const long long need = ((long long)lk[i] + kMaxSplits - 1) / kMaxSplits;
-        if (chunk < need) chunk = (need + unit - 1) / unit * unit;
+        if (chunk < need) chunk = (need + kBlock - 1) / kBlock * kBlock;
     }
-    return (int)chunk;
-}
-
-// Floats of scratch a batch uses (<= the sum of decode_partials_len over its sequences).
-size_t decode_batch_scratch(const int* lk, int n, int chunk, int hq) {
-    size_t f = 0;
-    for (int i = 0; i < n; ++i) f += (size_t)hq * ((lk[i] + chunk - 1) / chunk) * (kDim + 2);
-    return f;
+    *chunk_out = (int)chunk;
+    *waves_out = waves;
 }
 
 int decode_batch_launch(const float* q, const void* const* k, const void* const* v,
@@ -594,14 +626,14 @@ int decode_batch_launch(const float* q, const void* const* k, const void* const*
                         int hkv, int kv, bool per_head, hipStream_t stream) {
     const int group = hq / hkv;
     const int G = per_head ? 1 : group;
-    const int groups_y = per_head ? hq : hkv;
-    const int waves = (kv == BRASA_KV_F16 && G <= 4) ? 8 : 4;  // waves_for<kv, G>
-    const int chunk = decode_chunk(lk, n, groups_y, 32 * waves);
+    const int ngroups = per_head ? hq : hkv;
+    int chunk, waves;
+    decode_plan(lk, n, ngroups, &chunk, &waves);
     const size_t oelem = o_f16 ? 2 : 4;
     size_t part_off = 0;
     for (int b0 = 0; b0 < n; b0 += kMaxSeqs) {
         const int nb = min(kMaxSeqs, n - b0);
-        DecodeArgs a;
+        DecodeArgs<kMaxSeqs> a;
         memset(&a, 0, sizeof(a));
         a.q = q + (size_t)b0 * hq * kDim;
         a.part = partials;
@@ -610,6 +642,7 @@ int decode_batch_launch(const float* q, const void* const* k, const void* const*
         a.hq = hq;
         a.hkv = hkv;
         a.group = group;
+        a.ngroups = ngroups;
         a.chunk = chunk;
         a.nseq = nb;
         a.scale = 1.0f / sqrtf(static_cast<float>(kDim));
@@ -636,17 +669,12 @@ int decode_batch_launch(const float* q, const void* const* k, const void* const*
             ra.part_off[i] = d.part_off;
             any_multi |= d.splits > 1;
         }
-        int st;
-        switch (kv) {
-            case BRASA_KV_F32: st = launch_g<BRASA_KV_F32>(a, G, groups_y, stream); break;
-            case BRASA_KV_F16: st = launch_g<BRASA_KV_F16>(a, G, groups_y, stream); break;
-            case BRASA_KV_Q8_0: st = launch_g<BRASA_KV_Q8_0>(a, G, groups_y, stream); break;
-            default: return set_error(BRASA_ERR_ARG, "decode: invalid kv type %d", kv);
-        }
+        int st = nb == 1 ? launch_kv(one_seq(a), kv, G, waves, stream)
+                         : launch_kv(a, kv, G, waves, stream);
         if (st != BRASA_OK) return st;
         if (!any_multi) continue;
-        hipLaunchKernelGGL(decode_reduce_kernel, dim3(hq, kDim / kRedSlice, nb), dim3(64), 0,
-                           stream, ra);
+        hipLaunchKernelGGL(decode_reduce_kernel, dim3(hq, kDim / kRedSlice, nb), dim3(kRedThreads),
+                           0, stream, ra);
         st = check_launch("decode_reduce_kernel");
         if (st != BRASA_OK) return st;
     }
