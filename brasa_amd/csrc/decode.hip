@@ -197,21 +197,27 @@ decode_kernel(DecodeArgs<NS> a) {
     const int kh = h0 / a.group;           // its KV head
     const int c16 = lane & 15;             // MFMA row/column index
     const int u = lane >> 4;               // MFMA k-group (8 of the 32 k-slots)
-    const bool colq = c16 < G;             // this lane's column is a query head
+    // The 16 MFMA columns: c < G is head h0 + c with the hi halves of the split operands,
+    // G <= c < 2 G the same head with the lo halves, the rest zero. Columns c and c ^ G add up
+    // to the f32-accurate product, so one MFMA does the work of the hi and lo passes.
+    const bool colq = c16 < G;             // this lane's column is a query head (hi half)
+    const bool col_lo = c16 >= G && c16 < 2 * G;
+    const int hcol = h0 + (c16 & (G - 1));
 
-    // ---- Q^T B-operands: column c = head h0 + c, k-step t holds dims 32 t + 8 u + j ----------
-    half8 qhi[4], qlo[4];
+    // ---- Q^T B-operand: k-step t holds dims 32 t + 8 u + j -----------------------------------
+    half8 qb[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         // unconditional 128-bit loads (a valid head for every lane), masked afterwards
-        const f32x4* qp = reinterpret_cast<const f32x4*>(
-            qseq + (size_t)(h0 + (colq ? c16 : 0)) * kDim + 32 * t + 8 * u);
+        const f32x4* qp = reinterpret_cast<const f32x4*>(qseq + (size_t)hcol * kDim + 32 * t + 8 * u);
         const f32x4 q0 = qp[0], q1 = qp[1];
-        const float sc = colq ? a.scale : 0.0f;
+        const float sc = (colq || col_lo) ? a.scale : 0.0f;
         const float x[8] = {as_f32(q0.x * sc), as_f32(q0.y * sc), as_f32(q0.z * sc),
                             as_f32(q0.w * sc), as_f32(q1.x * sc), as_f32(q1.y * sc),
                             as_f32(q1.z * sc), as_f32(q1.w * sc)};  // f32, as reference
-        split8(x, qhi[t], qlo[t]);
+        half8 hi, lo;
+        split8(x, hi, lo);
+        qb[t] = col_lo ? lo : hi;
     }
 
     const int s0 = split * a.chunk;
@@ -294,8 +300,7 @@ decode_kernel(DecodeArgs<NS> a) {
                     half8 kh8, unused;
                     b.k[kt][t].get(kh8, unused);
                     f32x4 p = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                    p = mfma16(kh8, qhi[t], p);
-                    p = mfma16(kh8, qlo[t], p);
+                    p = mfma16(kh8, qb[t], p);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const uint32_t w = (t < 2) ? b.ksc[kt][i].x : b.ksc[kt][i].y;
@@ -311,14 +316,19 @@ decode_kernel(DecodeArgs<NS> a) {
                 for (int t = 0; t < 4; ++t) {
                     half8 khi, klo;
                     b.k[kt][t].get(khi, klo);
-                    s = mfma16(khi, qhi[t], s);
-                    s = mfma16(khi, qlo[t], s);
-                    if constexpr (KS) s = mfma16(klo, qhi[t], s);
+                    s = mfma16(khi, qb[t], s);
+                    if constexpr (KS) s = mfma16(klo, qb[t], s);
                 }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) x[kt][i] = s[i];
             }
         }
+        // hi + lo columns: lanes c and c ^ G get the same sum (a + b == b + a), so both go
+        // through the softmax below with identical bits
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[kt][i] += __shfl_xor(x[kt][i], G, 64);
         // online softmax (exp2 domain), keys past the split masked
         float bm = -INFINITY;
 #pragma unroll
@@ -345,7 +355,7 @@ decode_kernel(DecodeArgs<NS> a) {
         for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
 
         // O^T += V^T P^T; P^T slot j of lane (c, u) is key kappa(u, j) = j < 4 ? 4u + j : 16 + 4u + j - 4
-        half8 phi[Q8 ? 4 : 1], plo[Q8 ? 4 : 1];
+        half8 pb[Q8 ? 4 : 1];  // P^T B-operand: hi halves in columns < G, lo halves in [G, 2 G)
         if constexpr (Q8) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
@@ -356,10 +366,14 @@ decode_kernel(DecodeArgs<NS> a) {
                     const uint16_t sc = (uint16_t)((g & 1) ? (w >> 16) : (w & 0xffffu));
                     pg[j] = as_f32(p[j] * __builtin_amdgcn_ldexpf(h2f(sc), -q8_exp(sc)));
                 }
-                split8(pg, phi[g], plo[g]);
+                half8 hi, lo;
+                split8(pg, hi, lo);
+                pb[g] = col_lo ? lo : hi;
             }
         } else {
-            split8(p, phi[0], plo[0]);
+            half8 hi, lo;
+            split8(p, hi, lo);
+            pb[0] = col_lo ? lo : hi;
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         const int trc = (c16 & 3), trj = (c16 >> 2);
@@ -387,8 +401,7 @@ decode_kernel(DecodeArgs<NS> a) {
                 const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)p1);
                 const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)p2);
                 const half8 va = __builtin_bit_cast(half8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
-                acc[dt] = mfma16(va, phi[g], acc[dt]);
-                if (part == 0) acc[dt] = mfma16(va, plo[g], acc[dt]);
+                acc[dt] = mfma16(va, pb[g], acc[dt]);
             }
         }
     };
@@ -419,6 +432,11 @@ decode_kernel(DecodeArgs<NS> a) {
     // ---- this wave's partial for its G heads: combine the 4 k-groups' denominators ---------
     lsum += __shfl_xor(lsum, 16, 64);
     lsum += __shfl_xor(lsum, 32, 64);
+    // O^T column c (hi halves of P) plus column c + G (lo halves)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[dt][i] += __shfl_xor(acc[dt][i], G, 64);
     if (!colq) return;
     const int hh = h0 + c16;
     const int splits = sd.splits;
