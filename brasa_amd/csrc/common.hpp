@@ -154,6 +154,20 @@ __device__ __forceinline__ void lds_dma16(const uint8_t* src, uint16_t* lds_wave
         : "v"(src), "s"(m0)
         : "memory");
 }
+// As lds_dma16 with the nontemporal hint, for data read exactly once (K/V rows).
+__device__ __forceinline__ void lds_dma16_nt(const uint8_t* src, uint16_t* lds_wave_base) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)lds_wave_base);
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dwordx4 %1, off nt\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(src), "s"(m0)
+        : "memory");
+}
 // As lds_dma16 with a uniform 64-bit base in SGPRs and a per-lane 32-bit byte offset.
 __device__ __forceinline__ void lds_dma16_s(const uint8_t* sbase, uint32_t voff,
                                             uint32_t lds_wave_base /* uniform LDS address */) {

@@ -24,6 +24,7 @@
 //     MFMA k-step is one group), V scales are folded into P per group; f32 caches are split
 //     hi + lo like Q.
 #include <cstring>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -468,15 +469,321 @@ decode_kernel(DecodeArgs<NS> a) {
     }
 }
 
+// ---- f16 caches: HPW head groups x KS key slices per workgroup, every load explicit -----------
+// Workgroup = HPW * KS wave64: HPW adjacent head groups (a KV head and its G query heads) x one
+// split of `chunk` keys. Wave (hl, ks) = (wave % HPW, wave / HPW) walks the 32-key blocks ks,
+// ks + KS, ks + 2 KS, ... of the split for head group hl, so at any time the workgroup reads HPW
+// adjacent KV heads' rows (HPW * 256 contiguous bytes per key: a workgroup that reads one head's
+// 256-byte rows at the 2 KB stride of the cache loads the HBM channels unevenly and was measured
+// ~20 % slower at 16K keys). A wave keeps up to kRing blocks in flight: K rows go from HBM into
+// registers (the MFMA A operand), V rows HBM -> LDS (global_load_lds_dwordx4, read transposed by
+// ds_read_tr16_b64), Q into registers. Every vector-memory instruction of the kernel is inline
+// asm, issued in a fixed order, so each wait is an exact count: block i is ready when the blocks
+// issued after it (at most kRing - 1, 16 instructions each) are the only ones pending. The wait
+// names the registers it guards as operands, so no use of them can be scheduled above it.
+// Block i + kRing is issued into block i's ring slot once block i has been computed.
+// Softmax: columns c < G hold the hi halves of the split Q / P operands, G <= c < 2 G the lo
+// halves; one DPP exchange adds them (the same bits in both lanes). The running max is lazy: the
+// reference point moves only when a block's max exceeds it by more than 2^8, so most blocks skip
+// the rescale of O. After the split the KS waves of each head group merge (m, l, acc) through LDS
+// and the workgroup writes one partial per query head (or the output when the sequence has one
+// split).
+constexpr int kRing = 2;                    // blocks in flight per wave (16 instructions each)
+constexpr int kMaxLdsWaves = 8;
+constexpr int kTileHalves = kBlock * kDim;  // one 32 x 128 f16 tile = 8 KB
+constexpr float kLazyRescale = 8.0f;        // log2 of the largest P value before a rescale
+
+__device__ __forceinline__ u32x4 ld16_asm(const uint8_t* p) {
+    u32x4 r;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+    return r;
+}
+__device__ __forceinline__ u32x4 ld16_nt_asm(const uint8_t* p) {
+    u32x4 r;
+    asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(r) : "v"(p) : "memory");
+    return r;
+}
+// s_waitcnt vmcnt(N) that also "redefines" the 8 K registers of a ring slot, so the compiler
+// cannot move a read of them above the wait.
+template <int N>
+__device__ __forceinline__ void wait_k(u32x4 (&k)[8]) {
+    asm volatile("s_waitcnt vmcnt(%8)"
+                 : "+v"(k[0]), "+v"(k[1]), "+v"(k[2]), "+v"(k[3]), "+v"(k[4]), "+v"(k[5]),
+                   "+v"(k[6]), "+v"(k[7])
+                 : "n"(N)
+                 : "memory");
+}
+// value of lane (lane ^ M) of the same 16-lane row, M in {1, 2, 4, 8}, through DPP
+template <int M>
+__device__ __forceinline__ float xor_row(float x, int c16) {
+    if constexpr (M == 1) return dpp<0xB1>(x);  // quad_perm [1, 0, 3, 2]
+    if constexpr (M == 2) return dpp<0x4E>(x);  // quad_perm [2, 3, 0, 1]
+    if constexpr (M == 8) return dpp<0x128>(x); // row_ror:8
+    // M == 4: lanes with bit 2 clear read lane + 4 (row_ror:12), the others lane - 4 (row_ror:4)
+    const float up = dpp<0x12C>(x), down = dpp<0x124>(x);
+    return (c16 & 4) ? down : up;
+}
+// max over the 4 rows of the wave (lanes l, l ^ 16, l ^ 32, l ^ 48)
+__device__ __forceinline__ float max_rows(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
+    x = fmaxf(__int_as_float(a[0]), __int_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+    return fmaxf(__int_as_float(b[0]), __int_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_rows(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
+    x = __int_as_float(a[0]) + __int_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+    return __int_as_float(b[0]) + __int_as_float(b[1]);
+}
+
+template <int G, int NS, int HPW, int KS>
+__global__ void __launch_bounds__(64 * HPW * KS)
+decode_f16_kernel(DecodeArgs<NS> a) {
+    constexpr int RB = 256;
+    constexpr int W = HPW * KS;
+    static_assert(W <= kMaxLdsWaves, "waves per workgroup");
+    __shared__ __attribute__((aligned(16))) uint16_t s_v[W][kRing][kTileHalves];
+
+    // 1-D grid, head-group rows innermost: consecutive workgroups read the same keys of
+    // adjacent KV heads
+    const int rows = (a.ngroups + HPW - 1) / HPW;
+    const int col = blockIdx.x / rows, row = blockIdx.x - col * rows;
+    const int si = seq_of(a, col);
+    const SeqDesc& sd = a.seq[si];
+    const int split = col - sd.split0;
+    const float* qseq = a.q + (size_t)si * a.hq * kDim;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int hl = wave % HPW, ks = wave / HPW;
+    const int hg = row * HPW + hl;  // this wave's head group
+    const bool hg_ok = hg < a.ngroups;
+    const int h0 = min(hg, a.ngroups - 1) * G;  // its first query head
+    const int kh = h0 / a.group;                 // its KV head
+    const int c16 = lane & 15;
+    const int u = lane >> 4;
+    const bool colq = c16 < G;
+    const bool col_lo = c16 >= G && c16 < 2 * G;
+
+    const int s0 = split * a.chunk;
+    const int s1 = min(sd.lk, s0 + a.chunk);
+    const int nblk = (s1 - s0 + kBlock - 1) / kBlock;
+    // this wave's blocks: ks, ks + KS, ...
+    const int nb = (hg_ok && nblk > ks) ? (nblk - ks + KS - 1) / KS : 0;
+    const size_t kstride = (size_t)a.hkv * RB;
+    const uint8_t* kbase = sd.k + (size_t)kh * RB;
+    const uint8_t* vbase = sd.v + (size_t)kh * RB;
+
+    // Q rows of this lane's column (dims 32 t + 8 u .. + 8 for t < 4), loaded first
+    u32x4 qr[8];
+    {
+        const uint8_t* qrow = reinterpret_cast<const uint8_t*>(qseq + (size_t)(h0 + (c16 & (G - 1))) * kDim);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            qr[2 * t] = ld16_asm(qrow + 4 * (32 * t + 8 * u));
+            qr[2 * t + 1] = ld16_asm(qrow + 4 * (32 * t + 8 * u + 4));
+        }
+    }
+    u32x4 kr[kRing][8];
+    // block i of this wave -> ring slot S: 8 K loads (tile row 16 kt + c16, dims 32 t + 8 u in
+    // register kt * 4 + t), then 8 V copies (instruction r: rows 4 r .. 4 r + 3; chunk c of row
+    // q stored at chunk c ^ 2 (q & 3))
+    auto issue = [&](auto slot_c, int i) {
+        constexpr int S = decltype(slot_c)::value;
+        const int jb = s0 + kBlock * (ks + KS * i);
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            const uint8_t* row = kbase + (size_t)min(jb + 16 * kt + c16, s1 - 1) * kstride + 16 * u;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) kr[S][4 * kt + t] = ld16_nt_asm(row + 64 * t);
+        }
+        uint16_t* vt = &s_v[wave][S][0];
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+            lds_dma16_nt(vbase + (size_t)min(jb + 4 * r + u, s1 - 1) * kstride + 16 * (c16 ^ (2 * u)),
+                         vt + 512 * r);
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    if (nb > 0) issue(I0{}, 0);
+    if (nb > 1) issue(I1{}, 1);
+    // Q was issued first: it has landed when at most the blocks' instructions are pending
+    switch (min(nb, kRing)) {
+        case 2: wait_k<32>(qr); break;
+        case 1: wait_k<16>(qr); break;
+        default: wait_k<0>(qr); break;
+    }
+
+    // ---- Q^T B-operand: k-step t holds dims 32 t + 8 u + j; column c < G: head h0 + c, hi half;
+    // G <= c < 2 G: the same head, lo half; other columns zero ------------------------------------
+    half8 qb[4];
+    {
+        const float sc = (colq || col_lo) ? a.scale : 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const f32x4 q0 = __builtin_bit_cast(f32x4, qr[2 * t]);
+            const f32x4 q1 = __builtin_bit_cast(f32x4, qr[2 * t + 1]);
+            const float x[8] = {as_f32(q0.x * sc), as_f32(q0.y * sc), as_f32(q0.z * sc),
+                                as_f32(q0.w * sc), as_f32(q1.x * sc), as_f32(q1.y * sc),
+                                as_f32(q1.z * sc), as_f32(q1.w * sc)};  // f32, as reference
+            half8 hi, lo;
+            split8(x, hi, lo);
+            qb[t] = col_lo ? lo : hi;
+        }
+    }
+
+    float mref = -INFINITY;  // reference point of this column's exponentials, log2 domain
+    float lsum = 0.0f;       // this lane's share of the column's softmax denominator
+    f32x4 acc[8];            // O^T rows 16 dt + 4 u + i, column c16
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int trc = (c16 & 3), trj = (c16 >> 2);
+
+    // One step computes block i from ring slot S and refills the slot with block i + kRing.
+    auto step = [&](auto slot_c, int i) {
+        constexpr int S = decltype(slot_c)::value;
+        // block i's 16 instructions were followed by those of the block after it in the ring
+        if (i + 1 < nb) wait_k<16>(kr[S]);
+        else wait_k<0>(kr[S]);
+        const int jb = s0 + kBlock * (ks + KS * i);
+        // S^T tiles: rows = keys jb + 16 kt + 4 u + r, column = head (hi / lo half)
+        float x[2][4];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            f32x4 sacc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) sacc = mfma16(as_half8(kr[S][4 * kt + t]), qb[t], sacc);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x[kt][r] = sacc[r];
+        }
+        // hi + lo: lanes c and c ^ G add the same two values, so both hold the same bits
+        float bm = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float v = x[kt][r] + xor_row<G>(x[kt][r], c16);
+                const bool ok = jb + 16 * kt + 4 * u + r < s1;
+                x[kt][r] = ok ? v * kLog2e : -INFINITY;
+                bm = fmaxf(bm, x[kt][r]);
+            }
+        bm = max_rows(bm);  // finite: key jb is valid
+        // lazy reference point: rescale O only when some column's max grew by more than 2^8
+        if (__builtin_amdgcn_ballot_w64(bm > mref + kLazyRescale) != 0) {
+            const float mn = fmaxf(mref, bm);
+            const float alpha = __builtin_amdgcn_exp2f(mref - mn);
+            mref = mn;
+            lsum *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+        }
+        float p[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) p[j] = __builtin_amdgcn_exp2f(x[j >> 2][j & 3] - mref);
+        float ps = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ps += p[j];
+        lsum += ps;
+        half8 pb;
+        {
+            half8 hi, lo;
+            split8(p, hi, lo);
+            pb = col_lo ? lo : hi;
+        }
+        // O^T += V^T P^T; P^T slot j of lane (c, u) is key j < 4 ? 4u + j : 16 + 4u + j - 4
+        const uint16_t* vt = &s_v[wave][S][0];
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            const int off = ((((2 * dt + (trc >> 1)) ^ (2 * trj))) << 3) + 4 * (trc & 1);
+            const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vt + (4 * u + trj) * kDim + off));
+            const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vt + (16 + 4 * u + trj) * kDim + off));
+            const half8 va = __builtin_bit_cast(half8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+            acc[dt] = mfma16(va, pb, acc[dt]);
+        }
+        if (i + kRing < nb) {
+            // the slot's LDS reads have returned (their values fed the MFMAs above) before the
+            // next block's copies into it are issued
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            asm volatile("" ::: "memory");
+            issue(slot_c, i + kRing);
+        }
+    };
+    for (int i0 = 0; i0 < nb; i0 += kRing) {
+        step(I0{}, i0);
+        if (i0 + 1 >= nb) break;
+        step(I1{}, i0 + 1);
+    }
+
+    // ---- merge the KS waves of each head group through LDS -------------------------------------
+    lsum = sum_rows(lsum);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[dt][r] += xor_row<G>(acc[dt][r], c16);
+    __syncthreads();  // every wave is done with its V slots (all copies waited for)
+    float* m_acc = reinterpret_cast<float*>(&s_v[0][0][0]);            // [wave][G][128]
+    float* m_ml = m_acc + W * G * kDim;                                // [wave][G][2]
+    if (colq) {
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+            *reinterpret_cast<f32x4*>(m_acc + (wave * G + c16) * kDim + 16 * dt + 4 * u) = acc[dt];
+        // a wave without blocks reports m = -inf and l = 0
+        if (u == 0) *reinterpret_cast<f32x2*>(m_ml + (wave * G + c16) * 2) = f32x2{mref, lsum};
+    }
+    __syncthreads();
+    const int splits = sd.splits;
+    for (int idx = threadIdx.x; idx < HPW * G * (kDim / 4); idx += 64 * W) {
+        const int d = 4 * (idx % (kDim / 4));
+        const int c = (idx / (kDim / 4)) % G;
+        const int hm = idx / (G * (kDim / 4));  // head group within the workgroup
+        if (row * HPW + hm >= a.ngroups) continue;
+        float M = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) M = fmaxf(M, m_ml[((k * HPW + hm) * G + c) * 2]);
+        f32x4 A = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        float L = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            const int wv = k * HPW + hm;
+            const float mw = m_ml[(wv * G + c) * 2];
+            const float e = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+            A += e * *reinterpret_cast<const f32x4*>(m_acc + (wv * G + c) * kDim + d);
+            L += e * m_ml[(wv * G + c) * 2 + 1];
+        }
+        const int hh = (row * HPW + hm) * G + c;
+        if (splits == 1) {
+            const float inv = 1.0f / L;
+            const f32x4 y = A * inv;
+            const size_t ob = ((size_t)si * a.hq + hh) * kDim + d;
+            if (a.o_f16) {
+                u32x2 w;
+                w.x = pack2(f2h(y.x), f2h(y.y));
+                w.y = pack2(f2h(y.z), f2h(y.w));
+                *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.o) + ob) = w;
+            } else {
+                *reinterpret_cast<f32x4*>(static_cast<float*>(a.o) + ob) = y;
+            }
+        } else {
+            *reinterpret_cast<f32x4*>(a.part + sd.part_off + ((size_t)hh * splits + split) * kDim + d) = A;
+            if (d == 0) {
+                float* ml_out = a.part + sd.part_off + (size_t)a.hq * splits * kDim;
+                *reinterpret_cast<f32x2*>(ml_out + ((size_t)hh * splits + split) * 2) = f32x2{M, L};
+            }
+        }
+    }
+}
+
 // Second pass (attn_decode_reduce, decode_attention.metal:68-84): one workgroup of 4 waves per
-// (head, 16-dim slice). Thread t owns float4 column t % 4 of the slice and splits t / 4 + 64 r;
-// it loads all of them at once and folds them with the running-max form of the split merge, so
-// the pass costs one memory round trip for up to 128 splits. The 64 split lanes are then merged
-// by xor shuffles and, across the 4 waves, through LDS, always in the same order.
-constexpr int kRedSlice = 16;                           // dims per workgroup
+// (query head, 32-dim quarter, sequence). Thread t owns dims 4 (t % 8) .. + 4 of the quarter and
+// the splits t / 8 + 32 j; it loads kRedPer of them per round trip and folds them with the
+// running-max form of the split merge, o = sum_s w_s acc_s / sum_s w_s l_s with
+// w_s = 2^(m_s - max m). The 8 split lanes of a wave are merged by a butterfly over lane bits 3, 4
+// and 5 (DPP and permlane swaps: both partners compute the same merge, so the bits agree) and the
+// 4 waves through LDS in a fixed order, so the result is reproducible bit for bit.
 constexpr int kRedThreads = 256;
-constexpr int kRedLanes = kRedThreads / (kRedSlice / 4);  // 64 split lanes
-constexpr int kRedPer = 2;                              // splits per lane per round
+constexpr int kRedDims = 32;                               // dims per workgroup
+constexpr int kRedLanes = kRedThreads / (kRedDims / 4);   // 32 split lanes
+constexpr int kRedPer = 4;                                 // splits per lane per round trip
 
 struct ReduceArgs {
     const float* part;
@@ -497,56 +804,73 @@ __device__ __forceinline__ void merge_split(float& M, f32x4& A, float& L, float 
     M = Mn;
 }
 
+// value of lane l ^ 8 (DPP row_ror:8), l ^ 16 (permlane16_swap), l ^ 32 (permlane32_swap)
+template <int M>
+__device__ __forceinline__ float lane_xor(float x, int lane) {
+    if constexpr (M == 8) {
+        return dpp<0x128>(x);
+    } else if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
+        return __int_as_float((lane & 16) ? r[0] : r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+        return __int_as_float((lane & 32) ? r[0] : r[1]);
+    }
+}
+template <int M>
+__device__ __forceinline__ void merge_lanes(float& Mx, f32x4& A, float& L, int lane) {
+    const float m1 = lane_xor<M>(Mx, lane), l1 = lane_xor<M>(L, lane);
+    const f32x4 a1 = f32x4{lane_xor<M>(A.x, lane), lane_xor<M>(A.y, lane), lane_xor<M>(A.z, lane),
+                           lane_xor<M>(A.w, lane)};
+    merge_split(Mx, A, L, m1, a1, l1);
+}
+
 __global__ void __launch_bounds__(kRedThreads) decode_reduce_kernel(ReduceArgs ra) {
     const int si = blockIdx.z;
     const int splits = ra.splits[si];
     if (splits == 1) return;  // the split kernel wrote this sequence's output
     const float* part = ra.part + ra.part_off[si];
-    const int hq = ra.hq, o_f16 = ra.o_f16;
-    const int h = blockIdx.x, d0 = blockIdx.y * kRedSlice;
-    const int t = threadIdx.x, oi = t & 3, sub = t >> 2;
+    const int hq = ra.hq;
+    const int h = blockIdx.x, d0 = kRedDims * blockIdx.y;
+    const int t = threadIdx.x, q4 = t & 7, sl = t >> 3;
     const int lane = t & 63, wave = t >> 6;
-    const f32x4* acc = reinterpret_cast<const f32x4*>(part + (size_t)h * splits * kDim + d0) + oi;
+    const f32x4* acc = reinterpret_cast<const f32x4*>(part + (size_t)h * splits * kDim + d0) + q4;
     const f32x2* ml = reinterpret_cast<const f32x2*>(part + (size_t)hq * splits * kDim) + (size_t)h * splits;
     float M = -INFINITY, L = 0.0f;
     f32x4 A = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int s0 = sub; s0 < splits; s0 += kRedLanes * kRedPer) {
+    for (int s0 = sl; s0 < splits; s0 += kRedLanes * kRedPer) {
         f32x2 mlv[kRedPer];
         f32x4 av[kRedPer];
 #pragma unroll
         for (int r = 0; r < kRedPer; ++r) {
-            const int s = min(s0 + kRedLanes * r, splits - 1);
-            mlv[r] = ml[s];
-            av[r] = acc[(size_t)s * (kDim / 4)];
+            const int sp = min(s0 + kRedLanes * r, splits - 1);
+            mlv[r] = ml[sp];
+            av[r] = acc[(size_t)sp * (kDim / 4)];
         }
 #pragma unroll
         for (int r = 0; r < kRedPer; ++r)
             if (s0 + kRedLanes * r < splits) merge_split(M, A, L, mlv[r].x, av[r], mlv[r].y);
     }
-    // lanes with the same column: xor 4, 8, 16, 32
-#pragma unroll
-    for (int x = 4; x <= 32; x <<= 1) {
-        const f32x4 a = f32x4{__shfl_xor(A.x, x, 64), __shfl_xor(A.y, x, 64),
-                              __shfl_xor(A.z, x, 64), __shfl_xor(A.w, x, 64)};
-        merge_split(M, A, L, __shfl_xor(M, x, 64), a, __shfl_xor(L, x, 64));
-    }
-    __shared__ f32x4 s_a[4][4];
-    __shared__ float s_m[4][4], s_l[4][4];
-    if (lane < 4) {
+    merge_lanes<8>(M, A, L, lane);
+    merge_lanes<16>(M, A, L, lane);
+    merge_lanes<32>(M, A, L, lane);
+    __shared__ f32x4 s_a[4][8];
+    __shared__ float s_m[4][8], s_l[4][8];
+    if (lane < 8) {
         s_a[wave][lane] = A;
         s_m[wave][lane] = M;
         s_l[wave][lane] = L;
     }
     __syncthreads();
-    if (t >= 4) return;
+    if (t >= 8) return;
     M = s_m[0][t];
     A = s_a[0][t];
     L = s_l[0][t];
 #pragma unroll
     for (int w = 1; w < 4; ++w) merge_split(M, A, L, s_m[w][t], s_a[w][t], s_l[w][t]);
     const f32x4 y = A / L;
-    const size_t off = ((size_t)si * hq + h) * kDim + d0 + 4 * oi;
-    if (o_f16) {
+    const size_t off = ((size_t)si * hq + h) * kDim + d0 + 4 * t;
+    if (ra.o_f16) {
         u32x2 w;
         w.x = pack2(f2h(y.x), f2h(y.y));
         w.y = pack2(f2h(y.z), f2h(y.w));
@@ -556,32 +880,57 @@ __global__ void __launch_bounds__(kRedThreads) decode_reduce_kernel(ReduceArgs r
     }
 }
 
+// Launch shape chosen by decode_plan: keys per split, and the workgroup layout (head groups x
+// key slices for f16 caches, head groups of one wave each for the other caches).
+struct Plan {
+    int chunk;
+    int waves;  // register-staged kernel: head groups per workgroup
+    int hpw;    // f16 kernel: head groups per workgroup
+    int ks;     // f16 kernel: key slices (waves) per head group
+};
+
+template <int G, int NS, int HPW, int KS>
+int launch_f16(const DecodeArgs<NS>& a, int cols, hipStream_t stream) {
+    const int rows = (a.ngroups + HPW - 1) / HPW;
+    hipLaunchKernelGGL((decode_f16_kernel<G, NS, HPW, KS>), dim3(cols * rows), dim3(64 * HPW * KS),
+                       0, stream, a);
+    return check_launch("decode_f16_kernel");
+}
+
 template <int KV, int G, int NS>
-int launch(const DecodeArgs<NS>& a, int waves, hipStream_t stream) {
+int launch(const DecodeArgs<NS>& a, const Plan& p, hipStream_t stream) {
     const int cols = a.seq[a.nseq - 1].split0 + a.seq[a.nseq - 1].splits;
-    const int rows = (a.ngroups + waves - 1) / waves;
-    hipLaunchKernelGGL((decode_kernel<KV, G, NS>), dim3(cols, rows), dim3(64 * waves), 0, stream, a);
-    return check_launch("decode_kernel");
+    if constexpr (KV == BRASA_KV_F16) {
+        if (p.hpw == 4 && p.ks == 2) return launch_f16<G, NS, 4, 2>(a, cols, stream);
+        if (p.hpw == 2 && p.ks == 4) return launch_f16<G, NS, 2, 4>(a, cols, stream);
+        if (p.hpw == 1 && p.ks == 8) return launch_f16<G, NS, 1, 8>(a, cols, stream);
+        if (p.hpw == 1 && p.ks == 4) return launch_f16<G, NS, 1, 4>(a, cols, stream);
+        return set_error(BRASA_ERR_UNSUPPORTED, "decode: layout %d x %d not compiled", p.hpw, p.ks);
+    } else {
+        const int rows = (a.ngroups + p.waves - 1) / p.waves;
+        hipLaunchKernelGGL((decode_kernel<KV, G, NS>), dim3(cols, rows), dim3(64 * p.waves), 0,
+                           stream, a);
+        return check_launch("decode_kernel");
+    }
 }
 
 template <int KV, int NS>
-int launch_g(const DecodeArgs<NS>& a, int G, int waves, hipStream_t stream) {
+int launch_g(const DecodeArgs<NS>& a, int G, const Plan& p, hipStream_t stream) {
     switch (G) {
-        case 1: return launch<KV, 1, NS>(a, waves, stream);
-        case 2: return launch<KV, 2, NS>(a, waves, stream);
-        case 4: return launch<KV, 4, NS>(a, waves, stream);
-        case 8: return launch<KV, 8, NS>(a, waves, stream);
+        case 1: return launch<KV, 1, NS>(a, p, stream);
+        case 2: return launch<KV, 2, NS>(a, p, stream);
+        case 4: return launch<KV, 4, NS>(a, p, stream);
+        case 8: return launch<KV, 8, NS>(a, p, stream);
     }
     return set_error(BRASA_ERR_UNSUPPORTED, "decode: GQA group %d not compiled", G);
 }
 
-
 template <int NS>
-int launch_kv(const DecodeArgs<NS>& a, int kv, int G, int waves, hipStream_t stream) {
+int launch_kv(const DecodeArgs<NS>& a, int kv, int G, const Plan& p, hipStream_t stream) {
     switch (kv) {
-        case BRASA_KV_F32: return launch_g<BRASA_KV_F32>(a, G, waves, stream);
-        case BRASA_KV_F16: return launch_g<BRASA_KV_F16>(a, G, waves, stream);
-        case BRASA_KV_Q8_0: return launch_g<BRASA_KV_Q8_0>(a, G, waves, stream);
+        case BRASA_KV_F32: return launch_g<BRASA_KV_F32>(a, G, p, stream);
+        case BRASA_KV_F16: return launch_g<BRASA_KV_F16>(a, G, p, stream);
+        case BRASA_KV_Q8_0: return launch_g<BRASA_KV_Q8_0>(a, G, p, stream);
     }
     return set_error(BRASA_ERR_ARG, "decode: invalid kv type %d", kv);
 }
@@ -606,37 +955,48 @@ DecodeArgs<1> one_seq(const DecodeArgs<kMaxSeqs>& a) {
 
 }  // namespace
 
-// Launch plan for a batch of sequences: one split length `chunk` (a multiple of 32 keys and at
-// least 128, so a sequence of lk keys has at most ceil(lk / 128) splits and its partials fit the
-// reference's decode_partials_len(hq, lk) floats), and `waves` head groups per workgroup (4, 2
-// or 1: the most that still gives about BRASA_DECODE_WGS workgroups, default 256 = one per CU).
+// Launch plan for a batch of sequences. Splits have one length `chunk` for every sequence (a
+// multiple of 32 keys and at least 128, so a sequence of lk keys has at most ceil(lk / 128)
+// splits and its partials fit the reference's decode_partials_len(hq, lk) floats), chosen so that
+// about BRASA_DECODE_WGS workgroups (default 256 = one per CU) cover the batch.
+// f16 caches: the most head groups per workgroup (4, 2, 1) that still reach that many
+// workgroups, each head group read by 8 / hpw waves (4 waves for one head group when a split has
+// at most 4 blocks). Other caches: up to kMaxWaves head groups, one wave each.
 // The plan depends only on the lengths and head counts, so results are reproducible bit for bit.
-void decode_plan(const int* lk, int n, int ngroups, int* chunk_out, int* waves_out) {
-    static const int target_wgs = [] {
-        const char* e = getenv("BRASA_DECODE_WGS");
-        const int v = e ? atoi(e) : 0;
-        return v > 0 ? v : 256;
-    }();
+Plan decode_plan(const int* lk, int n, int ngroups, int kv) {
+    const char* env = getenv("BRASA_DECODE_WGS");
+    const long long target = env && atoi(env) > 0 ? atoi(env) : 256;
     long long total = 0, max_splits = 0;
     for (int i = 0; i < n; ++i) {
         total += lk[i];
         max_splits += (lk[i] + kMinChunk - 1) / kMinChunk;
     }
-    int waves = kMaxWaves;
-    while (waves > 1 && max_splits * ((ngroups + waves - 1) / waves) < target_wgs) waves >>= 1;
-    const long long rows = (ngroups + waves - 1) / waves;
-    long long splits = (target_wgs + rows - 1) / rows;
+    Plan p{0, 1, 1, 4};
+    int per_wg = 1;  // head groups per workgroup
+    if (kv == BRASA_KV_F16) {
+        int hpw = 4;
+        while (hpw > 1 && max_splits * ((ngroups + hpw - 1) / hpw) < target) hpw >>= 1;
+        const char* fh = getenv("BRASA_DECODE_HPW");
+        if (fh && (atoi(fh) == 1 || atoi(fh) == 2 || atoi(fh) == 4)) hpw = atoi(fh);
+        p.hpw = per_wg = hpw;
+    } else {
+        int waves = kMaxWaves;
+        while (waves > 1 && max_splits * ((ngroups + waves - 1) / waves) < target) waves >>= 1;
+        p.waves = per_wg = waves;
+    }
+    const long long rows = (ngroups + per_wg - 1) / per_wg;
+    long long splits = (target + rows - 1) / rows;
     if (splits < 1) splits = 1;
     long long chunk = (total + splits - 1) / splits;
     chunk = (chunk + kBlock - 1) / kBlock * kBlock;
     if (chunk < kMinChunk) chunk = kMinChunk;
-    // at most kMaxSplits splits per sequence
-    for (int i = 0; i < n; ++i) {
+    for (int i = 0; i < n; ++i) {  // at most kMaxSplits splits per sequence
         const long long need = ((long long)lk[i] + kMaxSplits - 1) / kMaxSplits;
         if (chunk < need) chunk = (need + kBlock - 1) / kBlock * kBlock;
     }
-    *chunk_out = (int)chunk;
-    *waves_out = waves;
+    p.chunk = (int)chunk;
+    if (kv == BRASA_KV_F16) p.ks = (p.hpw == 1 && chunk <= 4 * kBlock) ? 4 : 8 / p.hpw;
+    return p;
 }
 
 int decode_batch_launch(const float* q, const void* const* k, const void* const* v,
@@ -645,8 +1005,8 @@ int decode_batch_launch(const float* q, const void* const* k, const void* const*
     const int group = hq / hkv;
     const int G = per_head ? 1 : group;
     const int ngroups = per_head ? hq : hkv;
-    int chunk, waves;
-    decode_plan(lk, n, ngroups, &chunk, &waves);
+    const Plan plan = decode_plan(lk, n, ngroups, kv);
+    const int chunk = plan.chunk;
     const size_t oelem = o_f16 ? 2 : 4;
     size_t part_off = 0;
     for (int b0 = 0; b0 < n; b0 += kMaxSeqs) {
@@ -687,11 +1047,11 @@ int decode_batch_launch(const float* q, const void* const* k, const void* const*
             ra.part_off[i] = d.part_off;
             any_multi |= d.splits > 1;
         }
-        int st = nb == 1 ? launch_kv(one_seq(a), kv, G, waves, stream)
-                         : launch_kv(a, kv, G, waves, stream);
+        int st = nb == 1 ? launch_kv(one_seq(a), kv, G, plan, stream)
+                         : launch_kv(a, kv, G, plan, stream);
         if (st != BRASA_OK) return st;
         if (!any_multi) continue;
-        hipLaunchKernelGGL(decode_reduce_kernel, dim3(hq, kDim / kRedSlice, nb), dim3(kRedThreads),
+        hipLaunchKernelGGL(decode_reduce_kernel, dim3(hq, kDim / kRedDims, nb), dim3(kRedThreads),
                            0, stream, ra);
         st = check_launch("decode_reduce_kernel");
         if (st != BRASA_OK) return st;
