@@ -314,32 +314,34 @@ __device__ __forceinline__ int kswz(int r, int c) { return c ^ (r & 15); }
 __device__ __forceinline__ int vswz(int r, int c) { return c ^ (4 * (r & 3)); }
 
 template <int HW, bool PS>
-__global__ void __launch_bounds__(kThreads, 2)
+__global__ void __launch_bounds__(2 * kThreads, 1)
 prefill_f16_kernel(PrefillArgs a) {
     constexpr int TPW = 32 * 4 / HW;
     constexpr int kTileBytes = kStageHalves * 2;
-    __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kStageHalves];
-    __shared__ __attribute__((aligned(16))) uint16_t s_vv[2][kStageHalves];
+    // [K / V][group][buffer]: each group streams its own 64-key tiles; K and V have their own
+    // double buffers because K of tile i is free after tile i's QK^T, V only after its PV
+    __shared__ __attribute__((aligned(16))) uint16_t s_kv[2][2][2][kStageHalves];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = wave >> 2;  // group g contracts the workgroup's tiles g, g + 2, g + 4, ...
+    const int qw = wave & 3;    // head and 32-query block, as in prefill_kernel
     const int col = lane & 31;
     const int u = lane >> 5;
 
-    // Work order: head groups fastest (they spread over the XCDs); query tiles heaviest first
-    // for the first half of the grid and lightest first for the second, so the two workgroups
-    // that share a CU (first and second wave of dispatch) carry about the same total work.
+    // Work order: head groups fastest (they spread over the XCDs), query tiles heaviest first
+    // (one workgroup per CU; a CU that finishes a light tile early takes the next one).
     const int hg = blockIdx.x;
-    const int half = (a.ntiles + 1) / 2;
-    const int y = (int)blockIdx.y;
-    const int tile = y < half ? a.ntiles - 1 - y : y - half;
-    const int h = hg * HW + (wave % HW);
+    const int tile = a.ntiles - 1 - (int)blockIdx.y;
+    const int h = hg * HW + (qw % HW);
     const int kh = (hg * HW) / a.group;
     const int t0 = tile * TPW;
-    const int tw0 = t0 + 32 * (wave / HW);
+    const int tw0 = t0 + 32 * (qw / HW);
     const int lk = a.pos0 + a.tokens;
     const int kend_wg = a.pos0 + min(t0 + TPW, a.tokens);
     const int kend_w = a.pos0 + min(tw0 + 32, a.tokens);
+    const int ntile = (kend_wg + kTile - 1) / kTile;   // 64-key tiles the workgroup reads
+    const int ng = (ntile - grp + 1) / 2;               // tiles of this wave's group
 
     const int tq = tw0 + col;
     const bool qvalid = tq < a.tokens;
@@ -363,9 +365,13 @@ prefill_f16_kernel(PrefillArgs a) {
 
     // lane-constant byte offsets: K operand rows (per k-step t), V^T tr16 sources (per dt),
     // DMA sources (per row quad r)
-    uint32_t koff[8], voff[4], kdo[4], vdo[4];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) koff[t] = col * 256 + 16 * kswz(col, 2 * t + u);
+    // K operand of k-step t: row col, logical chunk 2 t + u = physical chunk (2 t ^ c14) + x0
+    const uint32_t kcol = col * 256 + 16 * (u ^ (col & 1));
+    const int c14 = col & 14;
+    // (recomputed at each use from an opaque copy of c14: 2 VALU per MFMA instead of 8 live
+    // registers the compiler would otherwise hoist and spill)
+    auto koff = [&](int t, int c) { return kcol + 16 * ((2 * t) ^ c); };
+    uint32_t voff[4];
     {
         const int sl = lane & 15, j = sl >> 2;
         const int low = 2 * ((lane >> 4) & 1) + ((sl & 3) >> 1);
@@ -374,27 +380,36 @@ prefill_f16_kernel(PrefillArgs a) {
             voff[dt] = (4 * u + j) * 256 + 16 * (4 * (dt ^ j) + low) + 8 * (sl & 1);
     }
     const uint32_t rstride = (uint32_t)a.hkv * 256;
-    {
-        const int lrow = lane >> 4, lchunk = lane & 15;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = 16 * wave + 4 * r + lrow;
-            kdo[r] = row * rstride + 16 * kswz(row, lchunk);
-            vdo[r] = row * rstride + 16 * vswz(row, lchunk);
-        }
-    }
+    // DMA sources of row quad r (rows 16 qw + 4 r + lane / 16, chunk lane % 16 swizzled)
+    const int lrow = lane >> 4, lchunk = lane & 15;
+    auto kdo = [&](int r, int lr, int lc) {
+        const int row = 16 * qw + 4 * r + lr;
+        return (uint32_t)(row * rstride + 16 * kswz(row, lc));
+    };
+    auto vdo = [&](int r, int lr, int lc) {
+        const int row = 16 * qw + 4 * r + lr;
+        return (uint32_t)(row * rstride + 16 * vswz(row, lc));
+    };
     const uint8_t* kbase = a.k + (size_t)kh * 256;
     const uint8_t* vbase = a.v + (size_t)kh * 256;
-    const uint32_t lds_k = lds_addr(&s_k[0][0]) + wave * 16 * 256;
-    const uint32_t lds_v = lds_addr(&s_vv[0][0]) + wave * 16 * 256;
-    auto dma = [&](int kb, int buf) {
-        const uint8_t* kg = kbase + (size_t)kb * rstride;
-        const uint8_t* vg = vbase + (size_t)kb * rstride;
+    // the 4 waves of a group copy 16 rows each of the group's tiles
+    const uint32_t lds_k = lds_addr(&s_kv[0][grp][0][0]) + qw * 16 * 256;
+    const uint32_t lds_v = lds_addr(&s_kv[1][grp][0][0]) + qw * 16 * 256;
+    // tile i of this group = workgroup tile 2 i + grp, keys [kb(i), kb(i) + 64)
+    auto kb_of = [&](int i) { return (2 * i + grp) * kTile; };
+    auto dma_k = [&](int i) {
+        const uint8_t* g = kbase + (size_t)kb_of(i) * rstride;
+        int lr = lrow, lc = lchunk;
+        asm volatile("" : "+v"(lr), "+v"(lc));  // recomputed per use (see koff)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            lds_dma16_s(kg, kdo[r], lds_k + buf * kTileBytes + r * 1024);
-            lds_dma16_s(vg, vdo[r], lds_v + buf * kTileBytes + r * 1024);
-        }
+        for (int r = 0; r < 4; ++r) lds_dma16_s(g, kdo(r, lr, lc), lds_k + (i & 1) * kTileBytes + r * 1024);
+    };
+    auto dma_v = [&](int i) {
+        const uint8_t* g = vbase + (size_t)kb_of(i) * rstride;
+        int lr = lrow, lc = lchunk;
+        asm volatile("" : "+v"(lr), "+v"(lc));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) lds_dma16_s(g, vdo(r, lr, lc), lds_v + (i & 1) * kTileBytes + r * 1024);
     };
 
     f32x16 acc[4];
@@ -406,42 +421,91 @@ prefill_f16_kernel(PrefillArgs a) {
     float lsum = 0.0f;
     const int qabs = a.pos0 + tq;
     const float kGrow = 8.0f / kLog2e;  // rescale when the max grows by 2^8 in exp2 terms
+    f32x16 s[2];                        // S^T of the current tile (32-key sub-blocks)
+    half8 pb[4], plb[PS ? 4 : 1];       // P^T of the current tile, per 16-key k-step
 
-    auto stage = [&](int kb, auto bufc) {
-        constexpr int buf = decltype(bufc)::value;
-        const uint8_t* kt = reinterpret_cast<const uint8_t*>(&s_k[buf][0]);
-        const uint8_t* vt = reinterpret_cast<const uint8_t*>(&s_vv[buf][0]);
-        const int nsub = (kb + 32 < kend_w) ? 2 : 1;
-        const f32x16 zero = {};
-        f32x16 s[2];
+    // MFMA phase i: O += V(i - 1) P(i - 1)^T, then S(i) = K(i) Q^T (each part if it exists;
+    // P(i - 1) is dead before S(i) is written, which keeps the two out of registers together).
+    // Both 32-key sub-blocks are always contracted: keys past the diagonal are masked to
+    // -inf (P = 0), which keeps the tile code straight-line.
+    auto mphase = [&](int i) {
+        if (i > 0) {
+            // O^T += V^T P^T over the 4 16-key k-steps; each k-step's 8 transposed V reads are
+            // issued two k-steps ahead of its MFMAs (LDS latency under 8 waves is several MFMAs)
+            const uint8_t* vt = reinterpret_cast<const uint8_t*>(&s_kv[1][grp][(i - 1) & 1][0]);
+            half8 va[4][4];
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            if (b < nsub) {
-                s[b] = mfma(lds_b128(reinterpret_cast<const uint16_t*>(kt + koff[0] + b * 32 * 256)), qh[0], zero);
+            for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-                for (int t = 1; t < 8; ++t)
-                    s[b] = mfma(lds_b128(reinterpret_cast<const uint16_t*>(kt + koff[t] + b * 32 * 256)), qh[t], s[b]);
-            }
-        }
-        // causal mask (only on sub-blocks that reach past the wave's first query)
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            if (b < nsub) {
-                const int kb2 = kb + 32 * b;
-                if ((kb2 + 31 > a.pos0 + tw0) || (kb2 + 31 >= lk)) {
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const int key = kb2 + 8 * (i / 4) + 4 * u + (i % 4);
-                        s[b][i] = (key > qabs || key >= lk) ? -INFINITY : s[b][i];
-                    }
+                for (int dt = 0; dt < 4; ++dt) {
+                    const int rows = 16 * ks * 256;
+                    const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vt + voff[dt] + rows));
+                    const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vt + voff[dt] + rows + 8 * 256));
+                    va[ks][dt] = __builtin_bit_cast(half8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
                 }
 #pragma unroll
-                for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[b][i]);
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) {
+                    acc[dt] = mfma(va[ks][dt], pb[ks], acc[dt]);
+                    if (PS) acc[dt] = mfma(va[ks][dt], plb[ks], acc[dt]);
+                }
+            // reads of k-steps 0 and 1 first, then one MFMA per 2 reads, then the rest
+            __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                __builtin_amdgcn_sched_group_barrier(0x008, PS ? 2 : 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
             }
+            __builtin_amdgcn_sched_group_barrier(0x008, PS ? 16 : 8, 0);
         }
+        if (i < ng) {
+            const f32x16 zero = {};
+            const uint8_t* kt = reinterpret_cast<const uint8_t*>(&s_kv[0][grp][i & 1][0]);
+            int c = c14;
+            asm volatile("" : "+v"(c));
+            half8 ka[2][8];
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+                    ka[b][t] = lds_b128(reinterpret_cast<const uint16_t*>(kt + koff(t, c) + b * 32 * 256));
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                s[b] = mfma(ka[b][0], qh[0], zero);
+#pragma unroll
+                for (int t = 1; t < 8; ++t) s[b] = mfma(ka[b][t], qh[t], s[b]);
+            }
+            // sub-block 0's 8 K reads first, then one MFMA per read of sub-block 1, then the rest
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 1);
+        }
+    };
+    // softmax phase i: mask, running max (lazy rescale of O), P(i) = exp(S(i) - m) in f16
+    auto vphase = [&](int i) {
+        const int kb = kb_of(i);
+        // keys past this wave's last query or past lk: only tiles that reach that far
+        if (kb + 63 > a.pos0 + tw0 || kb + 63 >= lk) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kb + 32 * b + 8 * (r / 4) + 4 * u + (r % 4);
+                    s[b][r] = (key > qabs || key >= lk) ? -INFINITY : s[b][r];
+                }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[b][r]);
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const bool grow = tmax > m_used + kGrow;
+        const bool grow = tmax > m_used + kGrow;  // false while the column has no key
         if (__builtin_amdgcn_ballot_w64(grow)) {
             const float alpha = grow ? __builtin_amdgcn_exp2f((m_used - tmax) * kLog2e) : 1.0f;
             if (grow) m_used = tmax;
@@ -449,61 +513,88 @@ prefill_f16_kernel(PrefillArgs a) {
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
+                for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
         }
-        const float mb = m_used * kLog2e;
+        // a column without a key so far (group 1's first tile for the first queries) has
+        // m = -inf and every s = -inf: P = 2^(-inf - 0) = 0
+        const float mb = m_used == -INFINITY ? 0.0f : m_used * kLog2e;
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            if (b >= nsub) break;
+        for (int ks = 0; ks < 4; ++ks) {
+            const int b = ks >> 1, st = ks & 1;
+            uint16_t ph[8], pl[8];
 #pragma unroll
-            for (int st = 0; st < 2; ++st) {
-                uint16_t ph[8], pl[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float p = __builtin_amdgcn_exp2f(fmaf(s[b][8 * st + j], kLog2e, -mb));
-                    lsum += p;
-                    if (PS) split_f16(p, ph[j], pl[j]);
-                    else ph[j] = f2h(p);
-                }
-                const half8 pb = pack8(ph);
-                half8 plb;
-                if (PS) plb = pack8(pl);
-                const int rows = (32 * b + 16 * st) * 256;
-#pragma unroll
-                for (int dt = 0; dt < 4; ++dt) {
-                    const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (lds_v4s*)(vt + voff[dt] + rows));
-                    const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (lds_v4s*)(vt + voff[dt] + rows + 8 * 256));
-                    const half8 va = __builtin_bit_cast(
-                        half8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
-                    acc[dt] = mfma(va, pb, acc[dt]);
-                    if (PS) acc[dt] = mfma(va, plb, acc[dt]);
-                }
+            for (int j = 0; j < 8; ++j) {
+                const float p = __builtin_amdgcn_exp2f(fmaf(s[b][8 * st + j], kLog2e, -mb));
+                lsum += p;
+                if (PS) split_f16(p, ph[j], pl[j]);
+                else ph[j] = f2h(p);
             }
+            pb[ks] = pack8(ph);
+            if (PS) plb[ks] = pack8(pl);
         }
     };
+    // copies issued after MFMA phase j: K(j + 2), then V(j + 1). Before MFMA phase i, K(i) and
+    // V(i - 1) (issued after phase i - 2) must have landed; only the copies issued after phase
+    // i - 1 (K(i + 1), V(i)) may still be in flight.
+    auto copies_after = [&](int j) {
+        if (j + 2 < ng) dma_k(j + 2);
+        if (j + 1 < ng) dma_v(j + 1);
+    };
+    auto wait_for = [&](int i) {
+        const int pend = 4 * (i + 1 < ng) + 4 * (i < ng);
+        if (pend == 8) wait_vmcnt<8>();
+        else if (pend == 4) wait_vmcnt<4>();
+        else wait_vmcnt<0>();
+    };
 
-    // stages alternate between the two LDS buffers; stage i + 1 streams in during stage i
-    dma(0, 0);
-    for (int kb = 0; kb < kend_wg; kb += 2 * kTile) {
-#pragma unroll
-        for (int half_i = 0; half_i < 2; ++half_i) {
-            const int kbi = kb + half_i * kTile;
-            if (kbi >= kend_wg) break;
-            __syncthreads();  // every wave is done with the buffer the next copy overwrites
-            if (kbi + kTile < kend_wg) {
-                dma(kbi + kTile, half_i ^ 1);
-                wait_vmcnt<8>();
-            } else {
-                wait_vmcnt<0>();
-            }
-            __syncthreads();
-            if (kbi < kend_w) {
-                if (half_i == 0) stage(kbi, std::integral_constant<int, 0>{});
-                else stage(kbi, std::integral_constant<int, 1>{});
-            }
+    // prologue: K(0), K(1), V(0)
+    if (0 < ng) dma_k(0);
+    if (1 < ng) dma_k(1);
+    if (0 < ng) dma_v(0);
+    // Both groups run the same loop (MFMA phase k, barrier, softmax phase k, barrier); group 1
+    // passes one extra barrier before it and group 0 one after it, so the barrier counts match
+    // while group 1 runs one phase behind: each group's MFMA phase overlaps the other group's
+    // softmax phase.
+    const int niter = (ntile + 1) / 2 + 1;  // group 0's tiles + the final PV-only phase
+    if (grp == 1) __syncthreads();
+    for (int k = 0; k < niter; ++k) {
+        const bool on = k <= ng;
+        if (on) wait_for(k);
+        __syncthreads();
+        if (on) {
+            mphase(k);
+            copies_after(k);
         }
+        __syncthreads();
+        if (k < ng) vphase(k);
+    }
+    if (grp == 0) __syncthreads();
+    wait_vmcnt<0>();
+
+    // ---- merge the two groups' key halves: group 1 hands (m, l, O) to group 0 through LDS ---
+    __syncthreads();  // all tiles contracted, every copy waited for
+    float* xch = reinterpret_cast<float*>(&s_kv[0][0][0][0]) + (size_t)(qw * 64 + lane) * 67;
+    if (grp == 1) {
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) xch[16 * dt + i] = acc[dt][i];
+        xch[64] = m_used;
+        xch[65] = lsum;
+    }
+    __syncthreads();
+    if (grp == 1) return;
+    {
+        const float mb2 = xch[64], lb = xch[65];
+        const float M = fmaxf(m_used, mb2);
+        // a group that saw no key of this column has m = -inf and weight 0
+        const float wa = (m_used == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((m_used - M) * kLog2e);
+        const float wb = (mb2 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((mb2 - M) * kLog2e);
+        lsum = lsum * wa + lb * wb;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[dt][i] = acc[dt][i] * wa + xch[16 * dt + i] * wb;
     }
 
     const float L = lsum + __shfl_xor(lsum, 32, 64);
@@ -534,8 +625,8 @@ int launch(const PrefillArgs& a, hipStream_t stream) {
 
 template <int HW, bool PS>
 int launch_f16(const PrefillArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL((prefill_f16_kernel<HW, PS>), dim3(a.hq / HW, a.ntiles), dim3(kThreads), 0,
-                       stream, a);
+    hipLaunchKernelGGL((prefill_f16_kernel<HW, PS>), dim3(a.hq / HW, a.ntiles), dim3(2 * kThreads),
+                       0, stream, a);
     return check_launch("prefill_f16_kernel");
 }
 
