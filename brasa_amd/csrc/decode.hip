@@ -773,6 +773,357 @@ decode_f16_kernel(DecodeArgs<NS> a) {
     }
 }
 
+// ---- q8_0 caches: the f16 kernel's structure with codes and scales staged in LDS -----------
+// Same workgroup layout, plan, ring, explicit waits and split merge as decode_f16_kernel. A ring
+// slot holds one 32-key block of K and V in their storage form: codes (32 x 128 bytes each) and
+// the 4 f16 scales per row (32 x 8 bytes each), copied by 16-byte (codes) and 4-byte (scales)
+// global_load_lds; 10 copy instructions per block.
+//  * S^T = K Q^T: K codes are read in the MFMA A layout (16-byte chunk c of row r stored at
+//    c ^ ((r >> 1) & 7): conflict-free 8-byte reads), converted exactly to f16, and each 32-dim
+//    group (one MFMA k-step) gets its own accumulator, scaled by that row's group scale in f32:
+//    s = sum_g scale_g * (q . codes_g), the exact dequantised dot product up to f32 rounding.
+//  * O^T += V^T P^T: after the block's S, each lane converts 64 V codes to f16 times 2^e (exact:
+//    |code| <= 127, e <= 9) and writes them as the f16 V tile over the block's code area (the
+//    ds_read_tr16_b64 layout of the f16 kernel); the scale's mantissa factor scale * 2^-e is
+//    folded into P per 32-dim group, so every product stays exact up to the f32 accumulation.
+constexpr int kQ8Codes = kBlock * 128;        // bytes of one tile's codes
+constexpr int kQ8Fac = 2 * kQ8Codes + 2 * kBlock * 8;   // K codes, V codes, K scales, V scales,
+constexpr int kQ8Slot = kQ8Fac + kBlock * 4 * 4;         // then V mantissa factors [key][group]
+
+// 4-byte HBM -> LDS copy per lane (global_load_lds_dword, nontemporal): lane i writes lds + 4 i.
+__device__ __forceinline__ void lds_dma4_nt(const uint8_t* src, const void* lds_wave_base) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dword %1, off nt\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(src), "s"(m0)
+        : "memory");
+}
+
+// 4 int8 codes (one dword) -> 4 exact f16 values: f16 bits 0x6400 | (code + 128) encode
+// 1024 + code + 128, minus 1152 (exact in f16 for these integers)
+__device__ __forceinline__ void codes4_to_f16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    const uint32_t x = w ^ 0x80808080u;
+    const uint32_t l = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);  // [64, b1, 64, b0]
+    const uint32_t h = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);  // [64, b3, 64, b2]
+    typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+    const half2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, l) + bias);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, h) + bias);
+}
+
+template <int G, int NS, int HPW, int KS>
+__global__ void __launch_bounds__(64 * HPW * KS)
+decode_q8_kernel(DecodeArgs<NS> a) {
+    constexpr int RB = kQ8Row;
+    constexpr int W = HPW * KS;
+    static_assert(W <= kMaxLdsWaves, "waves per workgroup");
+    __shared__ __attribute__((aligned(16))) uint8_t s_slot[W][kRing][kQ8Slot];
+
+    const int rows = (a.ngroups + HPW - 1) / HPW;
+    const int col = blockIdx.x / rows, row = blockIdx.x - col * rows;
+    const int si = seq_of(a, col);
+    const SeqDesc& sd = a.seq[si];
+    const int split = col - sd.split0;
+    const float* qseq = a.q + (size_t)si * a.hq * kDim;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int hl = wave % HPW, ks = wave / HPW;
+    const int hg = row * HPW + hl;
+    const bool hg_ok = hg < a.ngroups;
+    const int h0 = min(hg, a.ngroups - 1) * G;
+    const int kh = h0 / a.group;
+    const int c16 = lane & 15;
+    const int u = lane >> 4;
+    const bool colq = c16 < G;
+    const bool col_lo = c16 >= G && c16 < 2 * G;
+
+    const int s0 = split * a.chunk;
+    const int s1 = min(sd.lk, s0 + a.chunk);
+    const int nblk = (s1 - s0 + kBlock - 1) / kBlock;
+    const int nb = (hg_ok && nblk > ks) ? (nblk - ks + KS - 1) / KS : 0;
+    const size_t kstride = (size_t)a.hkv * RB;
+    const uint8_t* kbase = sd.k + (size_t)kh * RB;
+    const uint8_t* vbase = sd.v + (size_t)kh * RB;
+
+    u32x4 qr[8];
+    {
+        const uint8_t* qrow = reinterpret_cast<const uint8_t*>(qseq + (size_t)(h0 + (c16 & (G - 1))) * kDim);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            qr[2 * t] = ld16_asm(qrow + 4 * (32 * t + 8 * u));
+            qr[2 * t + 1] = ld16_asm(qrow + 4 * (32 * t + 8 * u + 4));
+        }
+    }
+    // block i -> slot S: K codes (4 instructions, 8 rows each, swizzled), V codes (4, plain),
+    // K scales, V scales (one 4-byte instruction each: lane l -> row l / 2, dword l % 2)
+    auto issue = [&](auto slot_c, int i) {
+        constexpr int S = decltype(slot_c)::value;
+        const int jb = s0 + kBlock * (ks + KS * i);
+        uint8_t* sl = &s_slot[wave][S][0];
+        const int lr = lane >> 3, lc = lane & 7;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int rr = 8 * r + lr;
+            const uint8_t* src = kbase + (size_t)min(jb + rr, s1 - 1) * kstride + 16 * (lc ^ ((rr >> 1) & 7));
+            lds_dma16_nt(src, reinterpret_cast<uint16_t*>(sl + 1024 * r));
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int rr = 8 * r + lr;
+            lds_dma16_nt(vbase + (size_t)min(jb + rr, s1 - 1) * kstride + 16 * lc,
+                         reinterpret_cast<uint16_t*>(sl + kQ8Codes + 1024 * r));
+        }
+        const int sr = lane >> 1;
+        lds_dma4_nt(kbase + (size_t)min(jb + sr, s1 - 1) * kstride + 128 + 4 * (lane & 1), sl + 2 * kQ8Codes);
+        lds_dma4_nt(vbase + (size_t)min(jb + sr, s1 - 1) * kstride + 128 + 4 * (lane & 1), sl + 2 * kQ8Codes + 256);
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    if (nb > 0) issue(I0{}, 0);
+    if (nb > 1) issue(I1{}, 1);
+    switch (min(nb, kRing)) {
+        case 2: wait_k<20>(qr); break;
+        case 1: wait_k<10>(qr); break;
+        default: wait_k<0>(qr); break;
+    }
+
+    half8 qb[4];
+    {
+        const float sc = (colq || col_lo) ? a.scale : 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const f32x4 q0 = __builtin_bit_cast(f32x4, qr[2 * t]);
+            const f32x4 q1 = __builtin_bit_cast(f32x4, qr[2 * t + 1]);
+            const float x[8] = {as_f32(q0.x * sc), as_f32(q0.y * sc), as_f32(q0.z * sc),
+                                as_f32(q0.w * sc), as_f32(q1.x * sc), as_f32(q1.y * sc),
+                                as_f32(q1.z * sc), as_f32(q1.w * sc)};  // f32, as reference
+            half8 hi, lo;
+            split8(x, hi, lo);
+            qb[t] = col_lo ? lo : hi;
+        }
+    }
+
+    float mref = -INFINITY;
+    float lsum = 0.0f;
+    f32x4 acc[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int trc = (c16 & 3), trj = (c16 >> 2);
+    // V conversion: lane l owns row l / 2, dims 64 (l % 2) .. + 64 (groups 2 (l % 2), + 1)
+    const int vr = lane >> 1, vh = lane & 1;
+
+    auto step = [&](auto slot_c, int i) {
+        constexpr int S = decltype(slot_c)::value;
+        if (i + 1 < nb) wait_vmcnt<10>();
+        else wait_vmcnt<0>();
+        const int jb = s0 + kBlock * (ks + KS * i);
+        uint8_t* sl = &s_slot[wave][S][0];
+        const uint8_t* ksc = sl + 2 * kQ8Codes;
+        const uint8_t* vsc = sl + 2 * kQ8Codes + 256;
+        // S^T: per 32-dim group t one MFMA (codes as f16), scaled by the row's group scale
+        float x[2][4];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            const int r = 16 * kt + c16;
+            f32x4 part[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int L = 2 * t + (u >> 1);
+                const u32x2 c = *reinterpret_cast<const u32x2*>(sl + r * 128 + 16 * (L ^ ((r >> 1) & 7)) + 8 * (u & 1));
+                uint32_t h0l, h0h, h1l, h1h;
+                codes4_to_f16(c.x, h0l, h0h);
+                codes4_to_f16(c.y, h1l, h1h);
+                const u32x4 h = u32x4{h0l, h0h, h1l, h1h};
+                part[t] = mfma16(as_half8(h), qb[t], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+            }
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                // scales of S row 16 kt + 4 u + rr
+                const u32x2 sw = *reinterpret_cast<const u32x2*>(ksc + (16 * kt + 4 * u + rr) * 8);
+                float v = part[0][rr] * h2f((uint16_t)(sw.x & 0xffffu));
+                v = fmaf(part[1][rr], h2f((uint16_t)(sw.x >> 16)), v);
+                v = fmaf(part[2][rr], h2f((uint16_t)(sw.y & 0xffffu)), v);
+                v = fmaf(part[3][rr], h2f((uint16_t)(sw.y >> 16)), v);
+                x[kt][rr] = v;
+            }
+        }
+        float bm = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float v = x[kt][r] + xor_row<G>(x[kt][r], c16);
+                const bool ok = jb + 16 * kt + 4 * u + r < s1;
+                x[kt][r] = ok ? v * kLog2e : -INFINITY;
+                bm = fmaxf(bm, x[kt][r]);
+            }
+        bm = max_rows(bm);
+        if (__builtin_amdgcn_ballot_w64(bm > mref + kLazyRescale) != 0) {
+            const float mn = fmaxf(mref, bm);
+            const float alpha = __builtin_amdgcn_exp2f(mref - mn);
+            mref = mn;
+            lsum *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+        }
+        float p[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) p[j] = __builtin_amdgcn_exp2f(x[j >> 2][j & 3] - mref);
+        float ps = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ps += p[j];
+        lsum += ps;
+        // V codes -> f16 * 2^e tile over the block's code area (the f16 kernel's tr16 layout);
+        // the same lane also writes the mantissa factors scale * 2^-e of its row's two groups
+        // to the slot's factor table, read back below to fold them into P
+        float* fac = reinterpret_cast<float*>(sl + kQ8Fac);  // [key][group]
+        {
+            u32x4 vc[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                vc[j] = *reinterpret_cast<const u32x4*>(sl + kQ8Codes + vr * 128 + 64 * vh + 16 * j);
+            const uint32_t vs = *reinterpret_cast<const uint32_t*>(vsc + vr * 8 + 4 * vh);
+            const uint16_t sc2[2] = {(uint16_t)(vs & 0xffffu), (uint16_t)(vs >> 16)};
+            int ex[2];
+            float fm[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                ex[q] = q8_exp(sc2[q]);
+                fm[q] = __builtin_amdgcn_ldexpf(h2f(sc2[q]), -ex[q]);
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // every LDS read of the code area has returned
+            asm volatile("" ::: "memory");
+            *reinterpret_cast<f32x2*>(fac + vr * 4 + 2 * vh) = f32x2{fm[0], fm[1]};
+            uint16_t* vt = reinterpret_cast<uint16_t*>(sl);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+                const _Float16 p2 = (_Float16)__builtin_amdgcn_ldexpf(1.0f, ex[j >> 1]);
+                const half2 m2 = {p2, p2};
+                const uint32_t w[4] = {vc[j].x, vc[j].y, vc[j].z, vc[j].w};
+                uint32_t hv[8];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    uint32_t l, h;
+                    codes4_to_f16(w[e], l, h);
+                    hv[2 * e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, l) * m2);      // exact
+                    hv[2 * e + 1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, h) * m2);
+                }
+                // 16 codes = dims 64 vh + 16 j .. + 16: logical chunks 8 vh + 2 j, + 1 of row vr
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const int lc2 = 8 * vh + 2 * j + q;
+                    *reinterpret_cast<u32x4*>(vt + vr * kDim + 8 * (lc2 ^ (2 * (vr & 3)))) =
+                        u32x4{hv[4 * q], hv[4 * q + 1], hv[4 * q + 2], hv[4 * q + 3]};
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // tile and factors written before they are read
+            asm volatile("" ::: "memory");
+        }
+        // P^T per 32-dim group g: p times the mantissa factor of the key's V scale, hi / lo split
+        half8 pb[4];
+        {
+            f32x4 fk[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int key = (j < 4) ? 4 * u + j : 16 + 4 * u + (j - 4);
+                fk[j] = *reinterpret_cast<const f32x4*>(fac + key * 4);
+            }
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                float pg[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) pg[j] = as_f32(p[j] * fk[j][g]);
+                half8 hi, lo;
+                split8(pg, hi, lo);
+                pb[g] = col_lo ? lo : hi;
+            }
+        }
+        const uint16_t* vt = reinterpret_cast<const uint16_t*>(sl);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            const int off = ((((2 * dt + (trc >> 1)) ^ (2 * trj))) << 3) + 4 * (trc & 1);
+            const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vt + (4 * u + trj) * kDim + off));
+            const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vt + (16 + 4 * u + trj) * kDim + off));
+            const half8 va = __builtin_bit_cast(half8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+            acc[dt] = mfma16(va, pb[dt >> 1], acc[dt]);
+        }
+        if (i + kRing < nb) {
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the slot's reads have returned
+            asm volatile("" ::: "memory");
+            issue(slot_c, i + kRing);
+        }
+    };
+    for (int i0 = 0; i0 < nb; i0 += kRing) {
+        step(I0{}, i0);
+        if (i0 + 1 >= nb) break;
+        step(I1{}, i0 + 1);
+    }
+
+    // ---- merge the KS waves of each head group through LDS -------------------------------------
+    lsum = sum_rows(lsum);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[dt][r] += xor_row<G>(acc[dt][r], c16);
+    __syncthreads();  // every wave is done with its V slots (all copies waited for)
+    float* m_acc = reinterpret_cast<float*>(&s_slot[0][0][0]);         // [wave][G][128]
+    float* m_ml = m_acc + W * G * kDim;                                // [wave][G][2]
+    if (colq) {
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+            *reinterpret_cast<f32x4*>(m_acc + (wave * G + c16) * kDim + 16 * dt + 4 * u) = acc[dt];
+        // a wave without blocks reports m = -inf and l = 0
+        if (u == 0) *reinterpret_cast<f32x2*>(m_ml + (wave * G + c16) * 2) = f32x2{mref, lsum};
+    }
+    __syncthreads();
+    const int splits = sd.splits;
+    for (int idx = threadIdx.x; idx < HPW * G * (kDim / 4); idx += 64 * W) {
+        const int d = 4 * (idx % (kDim / 4));
+        const int c = (idx / (kDim / 4)) % G;
+        const int hm = idx / (G * (kDim / 4));  // head group within the workgroup
+        if (row * HPW + hm >= a.ngroups) continue;
+        float M = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) M = fmaxf(M, m_ml[((k * HPW + hm) * G + c) * 2]);
+        f32x4 A = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        float L = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            const int wv = k * HPW + hm;
+            const float mw = m_ml[(wv * G + c) * 2];
+            const float e = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+            A += e * *reinterpret_cast<const f32x4*>(m_acc + (wv * G + c) * kDim + d);
+            L += e * m_ml[(wv * G + c) * 2 + 1];
+        }
+        const int hh = (row * HPW + hm) * G + c;
+        if (splits == 1) {
+            const float inv = 1.0f / L;
+            const f32x4 y = A * inv;
+            const size_t ob = ((size_t)si * a.hq + hh) * kDim + d;
+            if (a.o_f16) {
+                u32x2 w;
+                w.x = pack2(f2h(y.x), f2h(y.y));
+                w.y = pack2(f2h(y.z), f2h(y.w));
+                *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.o) + ob) = w;
+            } else {
+                *reinterpret_cast<f32x4*>(static_cast<float*>(a.o) + ob) = y;
+            }
+        } else {
+            *reinterpret_cast<f32x4*>(a.part + sd.part_off + ((size_t)hh * splits + split) * kDim + d) = A;
+            if (d == 0) {
+                float* ml_out = a.part + sd.part_off + (size_t)a.hq * splits * kDim;
+                *reinterpret_cast<f32x2*>(ml_out + ((size_t)hh * splits + split) * 2) = f32x2{M, L};
+            }
+        }
+    }
+}
+
 // Second pass (attn_decode_reduce, decode_attention.metal:68-84): one workgroup of 4 waves per
 // (query head, 32-dim quarter, sequence). Thread t owns dims 4 (t % 8) .. + 4 of the quarter and
 // the splits t / 8 + 32 j; it loads kRedPer of them per round trip and folds them with the
@@ -897,6 +1248,14 @@ int launch_f16(const DecodeArgs<NS>& a, int cols, hipStream_t stream) {
     return check_launch("decode_f16_kernel");
 }
 
+template <int G, int NS, int HPW, int KS>
+int launch_q8(const DecodeArgs<NS>& a, int cols, hipStream_t stream) {
+    const int rows = (a.ngroups + HPW - 1) / HPW;
+    hipLaunchKernelGGL((decode_q8_kernel<G, NS, HPW, KS>), dim3(cols * rows), dim3(64 * HPW * KS),
+                       0, stream, a);
+    return check_launch("decode_q8_kernel");
+}
+
 template <int KV, int G, int NS>
 int launch(const DecodeArgs<NS>& a, const Plan& p, hipStream_t stream) {
     const int cols = a.seq[a.nseq - 1].split0 + a.seq[a.nseq - 1].splits;
@@ -905,6 +1264,12 @@ int launch(const DecodeArgs<NS>& a, const Plan& p, hipStream_t stream) {
         if (p.hpw == 2 && p.ks == 4) return launch_f16<G, NS, 2, 4>(a, cols, stream);
         if (p.hpw == 1 && p.ks == 8) return launch_f16<G, NS, 1, 8>(a, cols, stream);
         if (p.hpw == 1 && p.ks == 4) return launch_f16<G, NS, 1, 4>(a, cols, stream);
+        return set_error(BRASA_ERR_UNSUPPORTED, "decode: layout %d x %d not compiled", p.hpw, p.ks);
+    } else if constexpr (KV == BRASA_KV_Q8_0) {
+        if (p.hpw == 4 && p.ks == 2) return launch_q8<G, NS, 4, 2>(a, cols, stream);
+        if (p.hpw == 2 && p.ks == 4) return launch_q8<G, NS, 2, 4>(a, cols, stream);
+        if (p.hpw == 1 && p.ks == 8) return launch_q8<G, NS, 1, 8>(a, cols, stream);
+        if (p.hpw == 1 && p.ks == 4) return launch_q8<G, NS, 1, 4>(a, cols, stream);
         return set_error(BRASA_ERR_UNSUPPORTED, "decode: layout %d x %d not compiled", p.hpw, p.ks);
     } else {
         const int rows = (a.ngroups + p.waves - 1) / p.waves;
@@ -973,7 +1338,7 @@ Plan decode_plan(const int* lk, int n, int ngroups, int kv) {
     }
     Plan p{0, 1, 1, 4};
     int per_wg = 1;  // head groups per workgroup
-    if (kv == BRASA_KV_F16) {
+    if (kv == BRASA_KV_F16 || kv == BRASA_KV_Q8_0) {
         int hpw = 4;
         while (hpw > 1 && max_splits * ((ngroups + hpw - 1) / hpw) < target) hpw >>= 1;
         const char* fh = getenv("BRASA_DECODE_HPW");
@@ -995,7 +1360,7 @@ Plan decode_plan(const int* lk, int n, int ngroups, int kv) {
         if (chunk < need) chunk = (need + kBlock - 1) / kBlock * kBlock;
     }
     p.chunk = (int)chunk;
-    if (kv == BRASA_KV_F16) p.ks = (p.hpw == 1 && chunk <= 4 * kBlock) ? 4 : 8 / p.hpw;
+    if (kv == BRASA_KV_F16 || kv == BRASA_KV_Q8_0) p.ks = (p.hpw == 1 && chunk <= 4 * kBlock) ? 4 : 8 / p.hpw;
     return p;
 }
 
