@@ -293,8 +293,8 @@ def profile_run(k: Kernels, stream: Stream, what: str) -> int:
     stream.synchronize()
     src.free()
     dst.free()
-    if what == "decode":
-        layers = DecodeLayers(k, 16384, KvType.F16, stream)
+    if what in ("decode", "decode_q8"):
+        layers = DecodeLayers(k, 16384, KvType.F16 if what == "decode" else KvType.Q8_0, stream)
         for _ in range(3):
             layers.step(stream)
         stream.synchronize()
@@ -312,7 +312,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="only the headline decode + 2K prefill")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--profile", choices=("decode", "prefill"),
+    ap.add_argument("--profile", choices=("decode", "decode_q8", "prefill"),
                     help="short fixed run for rocprofv3 (kernel trace / counters), no JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
