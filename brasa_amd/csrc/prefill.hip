@@ -616,6 +616,221 @@ prefill_f16_kernel(PrefillArgs a) {
     }
 }
 
+// Four-wave variant (one group, no key split), two workgroups per CU: with many query tiles per
+// CU (long prompts) the second workgroup on each CU gives the overlap that the two key groups of
+// prefill_f16_kernel give for short ones, without their merge and per-phase barriers.
+template <int HW, bool PS>
+__global__ void __launch_bounds__(kThreads, 2)
+prefill_f16_kernel4(PrefillArgs a) {
+    constexpr int TPW = 32 * 4 / HW;
+    constexpr int kTileBytes = kStageHalves * 2;
+    __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kStageHalves];
+    __shared__ __attribute__((aligned(16))) uint16_t s_vv[2][kStageHalves];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 31;
+    const int u = lane >> 5;
+
+    // Work order: head groups fastest (they spread over the XCDs); query tiles heaviest first
+    // for the first half of the grid and lightest first for the second, so the two workgroups
+    // that share a CU (first and second wave of dispatch) carry about the same total work.
+    const int hg = blockIdx.x;
+    const int half = (a.ntiles + 1) / 2;
+    const int y = (int)blockIdx.y;
+    const int tile = y < half ? a.ntiles - 1 - y : y - half;
+    const int h = hg * HW + (wave % HW);
+    const int kh = (hg * HW) / a.group;
+    const int t0 = tile * TPW;
+    const int tw0 = t0 + 32 * (wave / HW);
+    const int lk = a.pos0 + a.tokens;
+    const int kend_wg = a.pos0 + min(t0 + TPW, a.tokens);
+    const int kend_w = a.pos0 + min(tw0 + 32, a.tokens);
+
+    const int tq = tw0 + col;
+    const bool qvalid = tq < a.tokens;
+    half8 qh[8];
+    {
+        const float* qrow = a.q + ((size_t)(qvalid ? tq : 0) * a.hq + h) * kDim;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float4* p = reinterpret_cast<const float4*>(qrow + 16 * t + 8 * u);
+            const float4 x0 = p[0], x1 = p[1];
+            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            uint16_t hi[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float sx = as_f32(xs[j] * a.scale);  // f32 product, then f16
+                hi[j] = f2h(qvalid ? sx : 0.0f);
+            }
+            qh[t] = pack8(hi);
+        }
+    }
+
+    // lane-constant byte offsets: K operand rows (per k-step t), V^T tr16 sources (per dt),
+    // DMA sources (per row quad r)
+    uint32_t koff[8], voff[4], kdo[4], vdo[4];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) koff[t] = col * 256 + 16 * kswz(col, 2 * t + u);
+    {
+        const int sl = lane & 15, j = sl >> 2;
+        const int low = 2 * ((lane >> 4) & 1) + ((sl & 3) >> 1);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+            voff[dt] = (4 * u + j) * 256 + 16 * (4 * (dt ^ j) + low) + 8 * (sl & 1);
+    }
+    const uint32_t rstride = (uint32_t)a.hkv * 256;
+    {
+        const int lrow = lane >> 4, lchunk = lane & 15;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 16 * wave + 4 * r + lrow;
+            kdo[r] = row * rstride + 16 * kswz(row, lchunk);
+            vdo[r] = row * rstride + 16 * vswz(row, lchunk);
+        }
+    }
+    const uint8_t* kbase = a.k + (size_t)kh * 256;
+    const uint8_t* vbase = a.v + (size_t)kh * 256;
+    const uint32_t lds_k = lds_addr(&s_k[0][0]) + wave * 16 * 256;
+    const uint32_t lds_v = lds_addr(&s_vv[0][0]) + wave * 16 * 256;
+    auto dma = [&](int kb, int buf) {
+        const uint8_t* kg = kbase + (size_t)kb * rstride;
+        const uint8_t* vg = vbase + (size_t)kb * rstride;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            lds_dma16_s(kg, kdo[r], lds_k + buf * kTileBytes + r * 1024);
+            lds_dma16_s(vg, vdo[r], lds_v + buf * kTileBytes + r * 1024);
+        }
+    };
+
+    f32x16 acc[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[dt][i] = 0.0f;
+    float m_used = -INFINITY;  // shift of the column's exponentials (raw score units)
+    float lsum = 0.0f;
+    const int qabs = a.pos0 + tq;
+    const float kGrow = 8.0f / kLog2e;  // rescale when the max grows by 2^8 in exp2 terms
+
+    auto stage = [&](int kb, auto bufc) {
+        constexpr int buf = decltype(bufc)::value;
+        const uint8_t* kt = reinterpret_cast<const uint8_t*>(&s_k[buf][0]);
+        const uint8_t* vt = reinterpret_cast<const uint8_t*>(&s_vv[buf][0]);
+        const int nsub = (kb + 32 < kend_w) ? 2 : 1;
+        const f32x16 zero = {};
+        f32x16 s[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            if (b < nsub) {
+                s[b] = mfma(lds_b128(reinterpret_cast<const uint16_t*>(kt + koff[0] + b * 32 * 256)), qh[0], zero);
+#pragma unroll
+                for (int t = 1; t < 8; ++t)
+                    s[b] = mfma(lds_b128(reinterpret_cast<const uint16_t*>(kt + koff[t] + b * 32 * 256)), qh[t], s[b]);
+            }
+        }
+        // causal mask (only on sub-blocks that reach past the wave's first query)
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            if (b < nsub) {
+                const int kb2 = kb + 32 * b;
+                if ((kb2 + 31 > a.pos0 + tw0) || (kb2 + 31 >= lk)) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int key = kb2 + 8 * (i / 4) + 4 * u + (i % 4);
+                        s[b][i] = (key > qabs || key >= lk) ? -INFINITY : s[b][i];
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[b][i]);
+            }
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const bool grow = tmax > m_used + kGrow;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+            const float alpha = grow ? __builtin_amdgcn_exp2f((m_used - tmax) * kLog2e) : 1.0f;
+            if (grow) m_used = tmax;
+            lsum *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
+        }
+        const float mb = m_used * kLog2e;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            if (b >= nsub) break;
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                uint16_t ph[8], pl[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float p = __builtin_amdgcn_exp2f(fmaf(s[b][8 * st + j], kLog2e, -mb));
+                    lsum += p;
+                    if (PS) split_f16(p, ph[j], pl[j]);
+                    else ph[j] = f2h(p);
+                }
+                const half8 pb = pack8(ph);
+                half8 plb;
+                if (PS) plb = pack8(pl);
+                const int rows = (32 * b + 16 * st) * 256;
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) {
+                    const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_v4s*)(vt + voff[dt] + rows));
+                    const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_v4s*)(vt + voff[dt] + rows + 8 * 256));
+                    const half8 va = __builtin_bit_cast(
+                        half8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+                    acc[dt] = mfma(va, pb, acc[dt]);
+                    if (PS) acc[dt] = mfma(va, plb, acc[dt]);
+                }
+            }
+        }
+    };
+
+    // stages alternate between the two LDS buffers; stage i + 1 streams in during stage i
+    dma(0, 0);
+    for (int kb = 0; kb < kend_wg; kb += 2 * kTile) {
+#pragma unroll
+        for (int half_i = 0; half_i < 2; ++half_i) {
+            const int kbi = kb + half_i * kTile;
+            if (kbi >= kend_wg) break;
+            __syncthreads();  // every wave is done with the buffer the next copy overwrites
+            if (kbi + kTile < kend_wg) {
+                dma(kbi + kTile, half_i ^ 1);
+                wait_vmcnt<8>();
+            } else {
+                wait_vmcnt<0>();
+            }
+            __syncthreads();
+            if (kbi < kend_w) {
+                if (half_i == 0) stage(kbi, std::integral_constant<int, 0>{});
+                else stage(kbi, std::integral_constant<int, 1>{});
+            }
+        }
+    }
+
+    const float L = lsum + __shfl_xor(lsum, 32, 64);
+    if (!qvalid) return;
+    const float inv = 1.0f / L;
+    const size_t obase = ((size_t)tq * a.hq + h) * kDim;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = 32 * dt + 8 * g + 4 * u;
+            uint2 w;
+            w.x = (uint32_t)f2h(as_f32(acc[dt][4 * g] * inv)) |
+                  ((uint32_t)f2h(as_f32(acc[dt][4 * g + 1] * inv)) << 16);
+            w.y = (uint32_t)f2h(as_f32(acc[dt][4 * g + 2] * inv)) |
+                  ((uint32_t)f2h(as_f32(acc[dt][4 * g + 3] * inv)) << 16);
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.o) + obase + d) = w;
+        }
+    }
+}
+
 template <int KV, int HW, bool QS, bool PS, bool OF32>
 int launch(const PrefillArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL((prefill_kernel<KV, HW, QS, PS, OF32>), dim3(a.hq / HW, a.ntiles),
@@ -623,11 +838,20 @@ int launch(const PrefillArgs& a, hipStream_t stream) {
     return check_launch("prefill_kernel");
 }
 
+// Two-group kernel when the query tiles give at most ~2 workgroups per CU (it splits each tile's
+// keys over two wave groups), the four-wave kernel otherwise (measured: T = 512 at pos0 16384,
+// 128 workgroups: 273 vs 351 µs; T = 8192, 2048 workgroups: 721 vs 668 µs).
 template <int HW, bool PS>
 int launch_f16(const PrefillArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL((prefill_f16_kernel<HW, PS>), dim3(a.hq / HW, a.ntiles), dim3(2 * kThreads),
-                       0, stream, a);
-    return check_launch("prefill_f16_kernel");
+    const long long wgs = (long long)(a.hq / HW) * a.ntiles;
+    if (wgs <= 2 * 256) {
+        hipLaunchKernelGGL((prefill_f16_kernel<HW, PS>), dim3(a.hq / HW, a.ntiles),
+                           dim3(2 * kThreads), 0, stream, a);
+        return check_launch("prefill_f16_kernel");
+    }
+    hipLaunchKernelGGL((prefill_f16_kernel4<HW, PS>), dim3(a.hq / HW, a.ntiles), dim3(kThreads), 0,
+                       stream, a);
+    return check_launch("prefill_f16_kernel4");
 }
 
 template <int KV, int HW>
