@@ -9,9 +9,11 @@ from ._lib import BrasaError, LIB_PATH, build
 from .kernels import (DECODE_CHUNK, GQA_GROUPS, KV_ALIGN, AttnShape, Kernels, KvType, OutDType,
                       PrefillPrecision, RopeTable, decode_batch_partials_len, decode_partials_len, gqa_supported,
                       rope_table)
+from .kvcache import KvCache, kv_cache_bytes, kv_cache_len, kv_capacity, kv_offset
 
 __all__ = [
     "AttnShape", "BrasaError", "DECODE_CHUNK", "GQA_GROUPS", "KV_ALIGN", "Kernels", "KvType",
     "LIB_PATH", "OutDType", "PrefillPrecision", "RopeTable", "build", "decode_batch_partials_len", "decode_partials_len",
-    "gqa_supported", "rope_table",
+    "gqa_supported", "rope_table", "KvCache", "kv_cache_bytes", "kv_cache_len", "kv_capacity",
+    "kv_offset",
 ]

@@ -36,6 +36,9 @@ SYMBOLS = {
     "brasa_decode_partials_len": (SZ, [SZ, SZ]),
     "brasa_gqa_supported": (INT, [SZ, SZ]),
     "brasa_kv_bytes": (SZ, [INT, SZ]),
+    "brasa_kv_capacity": (SZ, [SZ]),
+    "brasa_kv_cache_len": (SZ, [SZ, SZ, SZ, SZ]),
+    "brasa_kv_offset": (SZ, [SZ, SZ, SZ, SZ, SZ]),
     "brasa_store_kv": (INT, [INT, VP, VP, SZ, VP]),
     "brasa_dequantize_kv_q8": (INT, [VP, VP, SZ, VP]),
     "brasa_decode_attention_lanes": (INT, [VP, VP, VP, VP, SZ, VP, INT, AttnShapeC, VP]),

@@ -76,6 +76,18 @@ size_t brasa_decode_partials_len(size_t hq, size_t lk) {
     return hq * ((lk + BRASA_DECODE_CHUNK - 1) / BRASA_DECODE_CHUNK) * 130;
 }
 
+size_t brasa_kv_capacity(size_t ctx) {
+    return (ctx + BRASA_KV_ALIGN - 1) / BRASA_KV_ALIGN * BRASA_KV_ALIGN;
+}
+
+size_t brasa_kv_cache_len(size_t layers, size_t ctx, size_t hkv, size_t dim) {
+    return layers * brasa_kv_capacity(ctx) * hkv * dim;
+}
+
+size_t brasa_kv_offset(size_t layer, size_t ctx, size_t hkv, size_t dim, size_t pos) {
+    return (layer * brasa_kv_capacity(ctx) + pos) * hkv * dim;
+}
+
 int brasa_gqa_supported(size_t hq, size_t hkv) {
     if (hkv == 0 || hq % hkv != 0) return 0;
     const size_t g = hq / hkv;

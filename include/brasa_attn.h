@@ -84,6 +84,19 @@ int brasa_gqa_supported(size_t hq, size_t hkv);
  * returns 0 and sets the error for an invalid type or a ragged q8_0 count. */
 size_t brasa_kv_bytes(int kv, size_t n);
 
+/* KV cache layout of the model (crates/models/src/qwen3.rs:384-386,554-556; the memory
+ * planner's kv_bytes, crates/memory/src/planner.rs:77-81). One layer holds
+ * cap = brasa_kv_capacity(ctx) positions of hkv x dim values; each of K and V is one buffer of
+ * brasa_kv_cache_len(layers, ctx, hkv, dim) elements (brasa_kv_bytes of that many bytes). */
+/* ctx rounded up to a multiple of BRASA_KV_ALIGN (ctx.next_multiple_of(KV_ALIGN)). */
+size_t brasa_kv_capacity(size_t ctx);
+/* layers * cap * hkv * dim: elements of the K (or V) cache buffer. */
+size_t brasa_kv_cache_len(size_t layers, size_t ctx, size_t hkv, size_t dim);
+/* (layer * cap + pos) * hkv * dim: element offset of position `pos` of `layer` (pos = 0 gives the
+ * layer base the attention entry points read; pos = pos0 the rows qk_norm_rope_store writes).
+ * The byte offset of the view is brasa_kv_bytes(kv, offset). */
+size_t brasa_kv_offset(size_t layer, size_t ctx, size_t hkv, size_t dim, size_t pos);
+
 /*
  * Kernels::store_kv (lib.rs:1029-1050; device code kv.metal:6-40): converts n f32 values at
  * `src` into the cache type at `dst`. f32: copy; f16: round to nearest even; q8_0: n must be a
