@@ -544,6 +544,9 @@ decode_f16_kernel(DecodeArgs<NS> a) {
     constexpr int W = HPW * KS;
     static_assert(W <= kMaxLdsWaves, "waves per workgroup");
     __shared__ __attribute__((aligned(16))) uint16_t s_v[W][kRing][kTileHalves];
+    constexpr int kMergeFloats = W * G * (kDim + 2);
+    constexpr bool kSepMerge = W * kRing * kTileHalves * 2 + kMergeFloats * 4 <= 160 * 1024;
+    __shared__ __attribute__((aligned(16))) float s_m[kSepMerge ? kMergeFloats : 1];
 
     // 1-D grid, head-group rows innermost: consecutive workgroups read the same keys of
     // adjacent KV heads
@@ -720,9 +723,16 @@ decode_f16_kernel(DecodeArgs<NS> a) {
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[dt][r] += xor_row<G>(acc[dt][r], c16);
-    __syncthreads();  // every wave is done with its V slots (all copies waited for)
-    float* m_acc = reinterpret_cast<float*>(&s_v[0][0][0]);            // [wave][G][128]
-    float* m_ml = m_acc + W * G * kDim;                                // [wave][G][2]
+    // The merge area has its own LDS when it fits beside the ring (one barrier); otherwise it
+    // reuses the V slots once every wave is done with them (all copies waited for).
+    float* m_acc;
+    if constexpr (kSepMerge) {
+        m_acc = s_m;
+    } else {
+        __syncthreads();
+        m_acc = reinterpret_cast<float*>(&s_v[0][0][0]);
+    }
+    float* m_ml = m_acc + W * G * kDim;  // m_acc: [wave][G][128], m_ml: [wave][G][2]
     if (colq) {
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
