@@ -80,6 +80,37 @@ __device__ __forceinline__ f32x16 mfma(half8 a, half8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// Q of one query column for the f16 kernels: 16 raw 16-byte loads per lane (k-step t holds
+// floats 16 t + 8 u .. + 8 of the row), all issued before anything else: the scheduling barrier
+// keeps the conversion (and its waits) below the first K/V copies the caller issues next, so Q
+// and those copies travel together instead of Q arriving in serial round trips first. The
+// compiler's own waits for these loads stay exact: they also cover any copy issued after them.
+__device__ __forceinline__ void q_load(const float* qrow, int u, u32x4 (&raw)[16]) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            raw[2 * t + h] = *reinterpret_cast<const u32x4*>(qrow + 16 * t + 8 * u + 4 * h);
+    __builtin_amdgcn_sched_barrier(0);
+}
+// f16(Q * scale) with the product in f32 (flash_attention.metal:213); zero for a padding column
+__device__ __forceinline__ void q_convert(const u32x4 (&raw)[16], float scale, bool valid,
+                                          half8 (&qh)[8]) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const f32x4 x0 = __builtin_bit_cast(f32x4, raw[2 * t]);
+        const f32x4 x1 = __builtin_bit_cast(f32x4, raw[2 * t + 1]);
+        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        uint16_t hi[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float sx = as_f32(xs[j] * scale);  // f32 product, then f16
+            hi[j] = f2h(valid ? sx : 0.0f);
+        }
+        qh[t] = pack8(hi);
+    }
+}
+
 // KV = cache type; HW = query heads per workgroup (1, 2, 4); QS = split Q (F32 precision);
 // PS = split P; OF32 = f32 output.
 template <int KV, int HW, bool QS, bool PS, bool OF32>
@@ -346,22 +377,8 @@ prefill_f16_kernel(PrefillArgs a) {
     const int tq = tw0 + col;
     const bool qvalid = tq < a.tokens;
     half8 qh[8];
-    {
-        const float* qrow = a.q + ((size_t)(qvalid ? tq : 0) * a.hq + h) * kDim;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const float4* p = reinterpret_cast<const float4*>(qrow + 16 * t + 8 * u);
-            const float4 x0 = p[0], x1 = p[1];
-            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            uint16_t hi[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float sx = as_f32(xs[j] * a.scale);  // f32 product, then f16
-                hi[j] = f2h(qvalid ? sx : 0.0f);
-            }
-            qh[t] = pack8(hi);
-        }
-    }
+    u32x4 qraw[16];
+    q_load(a.q + ((size_t)(qvalid ? tq : 0) * a.hq + h) * kDim, u, qraw);
 
     // lane-constant byte offsets: K operand rows (per k-step t), V^T tr16 sources (per dt),
     // DMA sources (per row quad r)
@@ -547,10 +564,11 @@ prefill_f16_kernel(PrefillArgs a) {
         else wait_vmcnt<0>();
     };
 
-    // prologue: K(0), K(1), V(0)
+    // prologue: K(0), K(1), V(0) right behind the Q loads, then the Q conversion
     if (0 < ng) dma_k(0);
     if (1 < ng) dma_k(1);
     if (0 < ng) dma_v(0);
+    q_convert(qraw, a.scale, qvalid, qh);
     // Both groups run the same loop (MFMA phase k, barrier, softmax phase k, barrier); group 1
     // passes one extra barrier before it and group 0 one after it, so the barrier counts match
     // while group 1 runs one phase behind: each group's MFMA phase overlaps the other group's
@@ -650,22 +668,8 @@ prefill_f16_kernel4(PrefillArgs a) {
     const int tq = tw0 + col;
     const bool qvalid = tq < a.tokens;
     half8 qh[8];
-    {
-        const float* qrow = a.q + ((size_t)(qvalid ? tq : 0) * a.hq + h) * kDim;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const float4* p = reinterpret_cast<const float4*>(qrow + 16 * t + 8 * u);
-            const float4 x0 = p[0], x1 = p[1];
-            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            uint16_t hi[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float sx = as_f32(xs[j] * a.scale);  // f32 product, then f16
-                hi[j] = f2h(qvalid ? sx : 0.0f);
-            }
-            qh[t] = pack8(hi);
-        }
-    }
+    u32x4 qraw[16];
+    q_load(a.q + ((size_t)(qvalid ? tq : 0) * a.hq + h) * kDim, u, qraw);
 
     // lane-constant byte offsets: K operand rows (per k-step t), V^T tr16 sources (per dt),
     // DMA sources (per row quad r)
@@ -790,8 +794,10 @@ prefill_f16_kernel4(PrefillArgs a) {
         }
     };
 
-    // stages alternate between the two LDS buffers; stage i + 1 streams in during stage i
+    // stages alternate between the two LDS buffers; stage i + 1 streams in during stage i.
+    // Stage 0's copies go out right behind the Q loads, then the Q conversion.
     dma(0, 0);
+    q_convert(qraw, a.scale, qvalid, qh);
     for (int kb = 0; kb < kend_wg; kb += 2 * kTile) {
 #pragma unroll
         for (int half_i = 0; half_i < 2; ++half_i) {
