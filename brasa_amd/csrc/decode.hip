@@ -108,6 +108,25 @@ __device__ __forceinline__ void split8(const float (&x)[8], half8& hi, half8& lo
     lo = as_half8(l);
 }
 
+// The half of split8 that one MFMA column takes: hi = f16(x), or lo = f16(x - hi) when `lo_part`
+// (bit for bit what split8 gives). Pairs go through one v_cvt_pk_f16_f32 each and the residual
+// x - hi is one exact fma with the f16 operand (it has at most 13 significant bits), so a lane
+// converts only what its column uses.
+__device__ __forceinline__ half8 split8_sel(const float (&x)[8], bool lo_part) {
+    typedef _Float16 hf2 __attribute__((ext_vector_type(2)));
+    typedef float ff2 __attribute__((ext_vector_type(2)));
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const ff2 v = {x[2 * i], x[2 * i + 1]};
+        const hf2 h = __builtin_convertvector(v, hf2);
+        const ff2 r = {fmaf((float)h.x, -1.0f, v.x), fmaf((float)h.y, -1.0f, v.y)};
+        const hf2 l = __builtin_convertvector(r, hf2);
+        w[i] = lo_part ? __builtin_bit_cast(uint32_t, l) : __builtin_bit_cast(uint32_t, h);
+    }
+    return as_half8(u32x4{w[0], w[1], w[2], w[3]});
+}
+
 // 8 int8 codes -> 8 f16 values (exact: |code| <= 127).
 __device__ __forceinline__ half8 codes_to_half8(u32x2 c) {
     u32x4 r;
@@ -687,12 +706,7 @@ decode_f16_kernel(DecodeArgs<NS> a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) ps += p[j];
         lsum += ps;
-        half8 pb;
-        {
-            half8 hi, lo;
-            split8(p, hi, lo);
-            pb = col_lo ? lo : hi;
-        }
+        const half8 pb = split8_sel(p, col_lo);
         // O^T += V^T P^T; P^T slot j of lane (c, u) is key j < 4 ? 4u + j : 16 + 4u + j - 4
         const uint16_t* vt = &s_v[wave][S][0];
 #pragma unroll
@@ -1049,9 +1063,7 @@ decode_q8_kernel(DecodeArgs<NS> a) {
                 float pg[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) pg[j] = as_f32(p[j] * fk[j][g]);
-                half8 hi, lo;
-                split8(pg, hi, lo);
-                pb[g] = col_lo ? lo : hi;
+                pb[g] = split8_sel(pg, col_lo);
             }
         }
         const uint16_t* vt = reinterpret_cast<const uint16_t*>(sl);
