@@ -127,36 +127,8 @@ __device__ __forceinline__ half8 split8_sel(const float (&x)[8], bool lo_part) {
     return as_half8(u32x4{w[0], w[1], w[2], w[3]});
 }
 
-// 8 int8 codes -> 8 f16 values (exact: |code| <= 127).
-__device__ __forceinline__ half8 codes_to_half8(u32x2 c) {
-    u32x4 r;
-    uint32_t w[2] = {c.x, c.y};
-    uint16_t h[8];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-            h[4 * i + b] = __half_as_ushort(__int2half_rn((int)(int8_t)((w[i] >> (8 * b)) & 0xffu)));
-    r.x = pack2(h[0], h[1]); r.y = pack2(h[2], h[3]); r.z = pack2(h[4], h[5]); r.w = pack2(h[6], h[7]);
-    return as_half8(r);
-}
-
-// One cache chunk of 8 consecutive dims as MFMA operand data: hi (and lo for f32 caches).
-template <int KV> struct Chunk;
-template <> struct Chunk<BRASA_KV_F16> {
-    static constexpr bool kSplit = false;
-    u32x4 raw;
-    __device__ __forceinline__ void load(const uint8_t* row, int d) { raw = ld_stream<u32x4>(row + 2 * d); }
-    __device__ __forceinline__ void get(half8& hi, half8&) const { hi = as_half8(raw); }
-};
-template <> struct Chunk<BRASA_KV_Q8_0> {
-    static constexpr bool kSplit = false;
-    u32x2 raw;
-    __device__ __forceinline__ void load(const uint8_t* row, int d) { raw = ld_stream<u32x2>(row + d); }
-    __device__ __forceinline__ void get(half8& hi, half8&) const { hi = codes_to_half8(raw); }
-};
-template <> struct Chunk<BRASA_KV_F32> {
-    static constexpr bool kSplit = true;
+// f32 caches: 8 consecutive dims of a row as MFMA operand data, split into hi and lo halves.
+struct F32Chunk {
     f32x4 a, b;
     __device__ __forceinline__ void load(const uint8_t* row, int d) {
         a = ld_stream<f32x4>(row + 4 * d);
@@ -168,14 +140,11 @@ template <> struct Chunk<BRASA_KV_F32> {
     }
 };
 
-// Per-block register state of one wave: K fragments (2 key tiles x 4 dim steps), V chunks
-// (8 rows of 4 per lane), and for q8_0 the f16 scales of the rows each lane needs.
-template <int KV> struct Block {
-    Chunk<KV> k[2][4];
-    Chunk<KV> v[8];
-    u32x2 ksc[2][4];   // q8_0: scales of S rows 16 kt + 4 u + i
-    u32x2 vsc[8];      // q8_0: scales of P slot keys kappa(u, j)
-    uint16_t vrs[8];   // q8_0: scale of V chunk i (row 4 i + u, group c16 / 4)
+// Per-block register state of one wave: K fragments (2 key tiles x 4 dim steps) and V chunks
+// (8 rows of 4 per lane).
+struct F32Block {
+    F32Chunk k[2][4];
+    F32Chunk v[8];
 };
 
 // A q8_0 scale s is applied as 2^e * (s * 2^-e), e = min(exponent(s), 9) (-14 for f16
@@ -186,24 +155,18 @@ __device__ __forceinline__ int q8_exp(uint16_t sc) {
     return e == 0 ? -14 : min(e - 15, 9);
 }
 
-template <int KV, int G, int NS>
+// ---- f32 caches (the reference's exact variant): register-staged K and V -------------------
+// One wave per head group and split. K and V rows are loaded into registers (the next block's
+// loads in flight while the current block is computed) and split into f16 hi + lo halves; V goes
+// through a wave-private padded LDS tile (hi and lo) to be read transposed.
+template <int G, int NS>
 __global__ void __launch_bounds__(64 * kMaxWaves)
-decode_kernel(DecodeArgs<NS> a) {
-    constexpr int RB = KvTraits<KV>::row_bytes;
-    constexpr bool KS = Chunk<KV>::kSplit;
-    constexpr bool Q8 = (KV == BRASA_KV_Q8_0);
-    constexpr int NV = KS ? 2 : 1;
+decode_f32_kernel(DecodeArgs<NS> a) {
+    constexpr int RB = KvTraits<BRASA_KV_F32>::row_bytes;
     constexpr int kWaves = kMaxWaves;
-    // f16 caches: V rows go HBM -> LDS directly (global_load_lds_dwordx4), double-buffered,
-    // 16-byte chunks XOR-swizzled by 2 * (row & 3) so the transposed reads are conflict-free.
-    // Other caches: V goes through registers (conversion), one padded tile (+ lo tile for f32).
-    constexpr bool DMA = (KV == BRASA_KV_F16);
-    constexpr int kVTile = DMA ? kBlock * kDim : NV * kBlock * kVStr;
+    constexpr int kVTile = 2 * kBlock * kVStr;
 
     __shared__ __attribute__((aligned(16))) uint16_t s_v[kWaves][kVTile];
-    // second V buffer of the DMA path, a distinct object so the compiler can tell its loads
-    // from the first buffer's when it places waits
-    __shared__ __attribute__((aligned(16))) uint16_t s_v2[kWaves][DMA ? kBlock * kDim : 8];
 
     const int si = seq_of(a, blockIdx.x);
     const SeqDesc& sd = a.seq[si];
@@ -246,47 +209,17 @@ decode_kernel(DecodeArgs<NS> a) {
     const uint8_t* kbase = sd.k + (size_t)kh * RB;
     const uint8_t* vbase = sd.v + (size_t)kh * RB;
     uint16_t* vt = &s_v[wave][0];
-    uint16_t* vt2 = &s_v2[wave][0];
 
-    auto load = [&](Block<KV>& b, int jb, int buf) {
+    auto load = [&](F32Block& b, int jb) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
             const uint8_t* row = kbase + (size_t)min(jb + 16 * kt + c16, s1 - 1) * kstride;
 #pragma unroll
             for (int t = 0; t < 4; ++t) b.k[kt][t].load(row, 32 * t + 8 * u);
         }
-        if constexpr (DMA) {
-            // instruction i fills LDS rows 4 i .. 4 i + 3 of buffer `buf`; lane (u, p) writes
-            // physical chunk p of row 4 i + u with logical chunk p ^ 2u
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                lds_dma16(vbase + (size_t)min(jb + 4 * i + u, s1 - 1) * kstride + 16 * (c16 ^ (2 * u)),
-                          (buf ? vt2 : vt) + 512 * i);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                b.v[i].load(vbase + (size_t)min(jb + 4 * i + u, s1 - 1) * kstride, 8 * c16);
-        }
-        if constexpr (Q8) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                b.vrs[i] = *reinterpret_cast<const uint16_t*>(
-                    vbase + (size_t)min(jb + 4 * i + u, s1 - 1) * kstride + 128 + 2 * (c16 >> 2));
-        }
-        if constexpr (Q8) {
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    b.ksc[kt][i] = *reinterpret_cast<const u32x2*>(
-                        kbase + (size_t)min(jb + 16 * kt + 4 * u + i, s1 - 1) * kstride + 128);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int key = (j < 4) ? 4 * u + j : 16 + 4 * u + (j - 4);
-                b.vsc[j] = *reinterpret_cast<const u32x2*>(
-                    vbase + (size_t)min(jb + key, s1 - 1) * kstride + 128);
-            }
-        }
+        for (int i = 0; i < 8; ++i)
+            b.v[i].load(vbase + (size_t)min(jb + 4 * i + u, s1 - 1) * kstride, 8 * c16);
     };
 
     float m2[1] = {-INFINITY};  // running max of the column's scores, log2 domain
@@ -295,53 +228,29 @@ decode_kernel(DecodeArgs<NS> a) {
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto compute = [&](const Block<KV>& b, int jb, int buf) {
-        // V rows -> wave-private LDS tile (row-major, 8 dims per lane and row)
+    auto compute = [&](const F32Block& b, int jb) {
+        // V rows -> wave-private LDS tiles (row-major, 8 dims per lane and row; hi then lo)
 #pragma unroll
-        for (int i = 0; i < (DMA ? 0 : 8); ++i) {
+        for (int i = 0; i < 8; ++i) {
             half8 hi, lo;
             b.v[i].get(hi, lo);
-            if constexpr (Q8) {
-                const _Float16 p2 = (_Float16)__builtin_amdgcn_ldexpf(1.0f, q8_exp(b.vrs[i]));
-#pragma unroll
-                for (int e = 0; e < 8; ++e) hi[e] = hi[e] * p2;  // exact: code * 2^e
-            }
             *reinterpret_cast<half8*>(&vt[(4 * i + u) * kVStr + 8 * c16]) = hi;
-            if constexpr (KS) *reinterpret_cast<half8*>(&vt[kBlock * kVStr + (4 * i + u) * kVStr + 8 * c16]) = lo;
+            *reinterpret_cast<half8*>(&vt[kBlock * kVStr + (4 * i + u) * kVStr + 8 * c16]) = lo;
         }
         // S^T tiles: rows = keys jb + 16 kt + 4 u + i, column = head
         float x[2][4];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
-            if constexpr (Q8) {
-                float sk[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            f32x4 s = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    half8 kh8, unused;
-                    b.k[kt][t].get(kh8, unused);
-                    f32x4 p = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                    p = mfma16(kh8, qb[t], p);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const uint32_t w = (t < 2) ? b.ksc[kt][i].x : b.ksc[kt][i].y;
-                        const float sc = h2f((uint16_t)((t & 1) ? (w >> 16) : (w & 0xffffu)));
-                        sk[i] = fmaf(p[i], sc, sk[i]);  // sum over groups of (q . codes) * scale
-                    }
-                }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) x[kt][i] = sk[i];
-            } else {
-                f32x4 s = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    half8 khi, klo;
-                    b.k[kt][t].get(khi, klo);
-                    s = mfma16(khi, qb[t], s);
-                    if constexpr (KS) s = mfma16(klo, qb[t], s);
-                }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) x[kt][i] = s[i];
+            for (int t = 0; t < 4; ++t) {
+                half8 khi, klo;
+                b.k[kt][t].get(khi, klo);
+                s = mfma16(khi, qb[t], s);
+                s = mfma16(klo, qb[t], s);
             }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[kt][i] = s[i];
         }
         // hi + lo columns: lanes c and c ^ G get the same sum (a + b == b + a), so both go
         // through the softmax below with identical bits
@@ -375,53 +284,22 @@ decode_kernel(DecodeArgs<NS> a) {
         for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
 
         // O^T += V^T P^T; P^T slot j of lane (c, u) is key kappa(u, j) = j < 4 ? 4u + j : 16 + 4u + j - 4
-        half8 pb[Q8 ? 4 : 1];  // P^T B-operand: hi halves in columns < G, lo halves in [G, 2 G)
-        if constexpr (Q8) {
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                float pg[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const uint32_t w = (g < 2) ? b.vsc[j].x : b.vsc[j].y;
-                    const uint16_t sc = (uint16_t)((g & 1) ? (w >> 16) : (w & 0xffffu));
-                    pg[j] = as_f32(p[j] * __builtin_amdgcn_ldexpf(h2f(sc), -q8_exp(sc)));
-                }
-                half8 hi, lo;
-                split8(pg, hi, lo);
-                pb[g] = col_lo ? lo : hi;
-            }
-        } else {
-            half8 hi, lo;
-            split8(p, hi, lo);
-            pb[0] = col_lo ? lo : hi;
-        }
+        // P^T B-operand: hi halves in columns < G, lo halves in [G, 2 G)
+        const half8 pb = split8_sel(p, col_lo);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         const int trc = (c16 & 3), trj = (c16 >> 2);
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
             const int col = 16 * dt + 4 * trc;
-            const int g = Q8 ? (dt >> 1) : 0;
 #pragma unroll
-            for (int part = 0; part < NV; ++part) {
-                const uint16_t *p1, *p2;
-                if constexpr (DMA) {
-                    // this tile's 8 DMA loads were followed by the next block's 8 K loads and
-                    // 8 DMA loads; vector-memory counts retire in order
-                    if (dt == 0) wait_vmcnt<16>();
-                    // swizzled rows of 128 halves: physical chunk = logical ^ 2 (row & 3)
-                    const uint16_t* base = buf ? vt2 : vt;
-                    const int off = ((((2 * dt + (trc >> 1)) ^ (2 * trj))) << 3) + 4 * (trc & 1);
-                    p1 = base + (4 * u + trj) * kDim + off;
-                    p2 = base + (16 + 4 * u + trj) * kDim + off;
-                } else {
-                    const uint16_t* base = vt + part * kBlock * kVStr;
-                    p1 = base + (4 * u + trj) * kVStr + col;
-                    p2 = base + (16 + 4 * u + trj) * kVStr + col;
-                }
+            for (int part = 0; part < 2; ++part) {  // V hi tile, then V lo tile
+                const uint16_t* base = vt + part * kBlock * kVStr;
+                const uint16_t* p1 = base + (4 * u + trj) * kVStr + col;
+                const uint16_t* p2 = base + (16 + 4 * u + trj) * kVStr + col;
                 const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)p1);
                 const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)p2);
                 const half8 va = __builtin_bit_cast(half8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
-                acc[dt] = mfma16(va, pb[g], acc[dt]);
+                acc[dt] = mfma16(va, pb, acc[dt]);
             }
         }
     };
@@ -429,24 +307,20 @@ decode_kernel(DecodeArgs<NS> a) {
     // ---- stream the split's 32-key blocks, the next block's loads in flight -----------------
     int jb = s0;
     {
-        Block<KV> A, B;
-        load(A, jb, 0);
+        F32Block A, B;
+        load(A, jb);
         // the prefetch is unconditional (rows clamp to s1 - 1): a branch around it would make
         // the compiler wait for every outstanding load before the current block's V writes
         while (true) {
-            load(B, jb + kBlock, 1);
-            compute(A, jb, 0);
+            load(B, jb + kBlock);
+            compute(A, jb);
             jb += kBlock;
             if (jb >= s1) break;
-            load(A, jb + kBlock, 0);
-            compute(B, jb, 1);
+            load(A, jb + kBlock);
+            compute(B, jb);
             jb += kBlock;
             if (jb >= s1) break;
         }
-        // The last prefetch's HBM -> LDS copies are still in flight. They must land before the
-        // wave ends: the workgroup's LDS is handed to the next workgroup on this CU when it
-        // exits, and a late copy would overwrite that workgroup's data.
-        if constexpr (DMA) wait_vmcnt<0>();
     }
 
     // ---- this wave's partial for its G heads: combine the 4 k-groups' denominators ---------
@@ -1295,9 +1169,9 @@ int launch(const DecodeArgs<NS>& a, const Plan& p, hipStream_t stream) {
         return set_error(BRASA_ERR_UNSUPPORTED, "decode: layout %d x %d not compiled", p.hpw, p.ks);
     } else {
         const int rows = (a.ngroups + p.waves - 1) / p.waves;
-        hipLaunchKernelGGL((decode_kernel<KV, G, NS>), dim3(cols, rows), dim3(64 * p.waves), 0,
+        hipLaunchKernelGGL((decode_f32_kernel<G, NS>), dim3(cols, rows), dim3(64 * p.waves), 0,
                            stream, a);
-        return check_launch("decode_kernel");
+        return check_launch("decode_f32_kernel");
     }
 }
 

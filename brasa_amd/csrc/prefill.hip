@@ -370,7 +370,6 @@ prefill_f16_kernel(PrefillArgs a) {
     const int tw0 = t0 + 32 * (qw / HW);
     const int lk = a.pos0 + a.tokens;
     const int kend_wg = a.pos0 + min(t0 + TPW, a.tokens);
-    const int kend_w = a.pos0 + min(tw0 + 32, a.tokens);
     const int ntile = (kend_wg + kTile - 1) / kTile;   // 64-key tiles the workgroup reads
     const int ng = (ntile - grp + 1) / 2;               // tiles of this wave's group
 
