@@ -836,6 +836,190 @@ prefill_f16_kernel4(PrefillArgs a) {
     }
 }
 
+// Three workgroups per CU: prefill_f16_kernel4's tile code on 32-key stages (32 KB of LDS per
+// workgroup) with the per-lane operand offsets recomputed at each use, so a wave fits 168
+// registers and each SIMD holds three waves. The kernel is latency-bound (matrix cores ~27 %
+// busy, LDS ~15 %): a third wave per SIMD hides more of the dependent chains. Query tiles
+// heaviest first; the dispatcher hands the light ones to CUs as they free up.
+constexpr int kTileS = 32;                    // keys per stage
+constexpr int kStageHalvesS = kTileS * kDim;  // one 32 x 128 f16 tile
+template <int HW, bool PS>
+__global__ void __launch_bounds__(kThreads, 3)
+prefill_f16_kernel4s(PrefillArgs a) {
+    constexpr int TPW = 32 * 4 / HW;
+    constexpr int kTileBytes = kStageHalvesS * 2;
+    __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kStageHalvesS];
+    __shared__ __attribute__((aligned(16))) uint16_t s_vv[2][kStageHalvesS];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 31;
+    const int u = lane >> 5;
+
+    const int hg = blockIdx.x;
+    const int tile = a.ntiles - 1 - (int)blockIdx.y;
+    const int h = hg * HW + (wave % HW);
+    const int kh = (hg * HW) / a.group;
+    const int t0 = tile * TPW;
+    const int tw0 = t0 + 32 * (wave / HW);
+    const int lk = a.pos0 + a.tokens;
+    const int kend_wg = a.pos0 + min(t0 + TPW, a.tokens);
+    const int kend_w = a.pos0 + min(tw0 + 32, a.tokens);
+
+    const int tq = tw0 + col;
+    const bool qvalid = tq < a.tokens;
+    half8 qh[8];
+    u32x4 qraw[16];
+    q_load(a.q + ((size_t)(qvalid ? tq : 0) * a.hq + h) * kDim, u, qraw);
+
+    // lane-constant byte offsets: K operand rows (recomputed per k-step from an opaque copy of
+    // the row, as in prefill_f16_kernel), V^T tr16 sources (per dt), DMA sources (per row pair)
+    const uint32_t kcol = col * 256 + 16 * (u ^ (col & 1));
+    const int c14 = col & 14;
+    auto koff = [&](int t, int c) { return kcol + 16 * ((2 * t) ^ c); };
+    uint32_t voff[4];
+    {
+        const int sl = lane & 15, j = sl >> 2;
+        const int low = 2 * ((lane >> 4) & 1) + ((sl & 3) >> 1);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+            voff[dt] = (4 * u + j) * 256 + 16 * (4 * (dt ^ j) + low) + 8 * (sl & 1);
+    }
+    const uint32_t rstride = (uint32_t)a.hkv * 256;
+    const uint8_t* kbase = a.k + (size_t)kh * 256;
+    const uint8_t* vbase = a.v + (size_t)kh * 256;
+    // each wave copies 8 rows of a 32-key stage: rows 8 wave + 4 r + lane / 16
+    const uint32_t lds_k = lds_addr(&s_k[0][0]) + wave * 8 * 256;
+    const uint32_t lds_v = lds_addr(&s_vv[0][0]) + wave * 8 * 256;
+    auto dma = [&](int kb, int buf) {
+        const uint8_t* kg = kbase + (size_t)kb * rstride;
+        const uint8_t* vg = vbase + (size_t)kb * rstride;
+        int lr = lane >> 4, lc = lane & 15;
+        asm volatile("" : "+v"(lr), "+v"(lc));  // recomputed per use
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int row = 8 * wave + 4 * r + lr;
+            lds_dma16_s(kg, (uint32_t)(row * rstride + 16 * kswz(row, lc)), lds_k + buf * kTileBytes + r * 1024);
+            lds_dma16_s(vg, (uint32_t)(row * rstride + 16 * vswz(row, lc)), lds_v + buf * kTileBytes + r * 1024);
+        }
+    };
+
+    f32x16 acc[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[dt][i] = 0.0f;
+    float m_used = -INFINITY;  // shift of the column's exponentials (raw score units)
+    float lsum = 0.0f;
+    const int qabs = a.pos0 + tq;
+    const float kGrow = 8.0f / kLog2e;  // rescale when the max grows by 2^8 in exp2 terms
+
+    auto stage = [&](int kb, auto bufc) {
+        constexpr int buf = decltype(bufc)::value;
+        const uint8_t* kt = reinterpret_cast<const uint8_t*>(&s_k[buf][0]);
+        const uint8_t* vt = reinterpret_cast<const uint8_t*>(&s_vv[buf][0]);
+        const f32x16 zero = {};
+        int c = c14;
+        asm volatile("" : "+v"(c));
+        f32x16 s = mfma(lds_b128(reinterpret_cast<const uint16_t*>(kt + koff(0, c))), qh[0], zero);
+#pragma unroll
+        for (int t = 1; t < 8; ++t)
+            s = mfma(lds_b128(reinterpret_cast<const uint16_t*>(kt + koff(t, c))), qh[t], s);
+        // causal mask (only on stages that reach past the wave's first query)
+        if ((kb + 31 > a.pos0 + tw0) || (kb + 31 >= lk)) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int key = kb + 8 * (i / 4) + 4 * u + (i % 4);
+                s[i] = (key > qabs || key >= lk) ? -INFINITY : s[i];
+            }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(tmax), __float_as_int(tmax), false, false);
+            tmax = fmaxf(__int_as_float(sw[0]), __int_as_float(sw[1]));
+        }
+        const bool grow = tmax > m_used + kGrow;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+            const float alpha = grow ? __builtin_amdgcn_exp2f((m_used - tmax) * kLog2e) : 1.0f;
+            if (grow) m_used = tmax;
+            lsum *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
+        }
+        // a column without a key so far has m = -inf and every s = -inf: P = 0
+        const float mb = m_used == -INFINITY ? 0.0f : m_used * kLog2e;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            uint16_t ph[8], pl[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float p = __builtin_amdgcn_exp2f(fmaf(s[8 * st + j], kLog2e, -mb));
+                lsum += p;
+                if (PS) split_f16(p, ph[j], pl[j]);
+                else ph[j] = f2h(p);
+            }
+            const half8 pb = pack8(ph);
+            half8 plb;
+            if (PS) plb = pack8(pl);
+            const int rows = 16 * st * 256;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vt + voff[dt] + rows));
+                const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vt + voff[dt] + rows + 8 * 256));
+                const half8 va = __builtin_bit_cast(half8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+                acc[dt] = mfma(va, pb, acc[dt]);
+                if (PS) acc[dt] = mfma(va, plb, acc[dt]);
+            }
+        }
+    };
+
+    // stages alternate between the two LDS buffers; stage i + 1 streams in during stage i.
+    // Stage 0's copies go out right behind the Q loads, then the Q conversion.
+    dma(0, 0);
+    q_convert(qraw, a.scale, qvalid, qh);
+    for (int kb = 0; kb < kend_wg; kb += 2 * kTileS) {
+#pragma unroll
+        for (int half_i = 0; half_i < 2; ++half_i) {
+            const int kbi = kb + half_i * kTileS;
+            if (kbi >= kend_wg) break;
+            __syncthreads();  // every wave is done with the buffer the next copy overwrites
+            if (kbi + kTileS < kend_wg) {
+                dma(kbi + kTileS, half_i ^ 1);
+                wait_vmcnt<4>();
+            } else {
+                wait_vmcnt<0>();
+            }
+            __syncthreads();
+            if (kbi < kend_w) {
+                if (half_i == 0) stage(kbi, std::integral_constant<int, 0>{});
+                else stage(kbi, std::integral_constant<int, 1>{});
+            }
+        }
+    }
+
+    const float L = lsum + __shfl_xor(lsum, 32, 64);
+    if (!qvalid) return;
+    const float inv = 1.0f / L;
+    const size_t obase = ((size_t)tq * a.hq + h) * kDim;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = 32 * dt + 8 * g + 4 * u;
+            uint2 w;
+            w.x = (uint32_t)f2h(as_f32(acc[dt][4 * g] * inv)) |
+                  ((uint32_t)f2h(as_f32(acc[dt][4 * g + 1] * inv)) << 16);
+            w.y = (uint32_t)f2h(as_f32(acc[dt][4 * g + 2] * inv)) |
+                  ((uint32_t)f2h(as_f32(acc[dt][4 * g + 3] * inv)) << 16);
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.o) + obase + d) = w;
+        }
+    }
+}
+
 template <int KV, int HW, bool QS, bool PS, bool OF32>
 int launch(const PrefillArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL((prefill_kernel<KV, HW, QS, PS, OF32>), dim3(a.hq / HW, a.ntiles),
@@ -843,16 +1027,26 @@ int launch(const PrefillArgs& a, hipStream_t stream) {
     return check_launch("prefill_kernel");
 }
 
-// Two-group kernel when the query tiles give at most ~2 workgroups per CU (it splits each tile's
-// keys over two wave groups), the four-wave kernel otherwise (measured: T = 512 at pos0 16384,
-// 128 workgroups: 273 vs 351 µs; T = 8192, 2048 workgroups: 721 vs 668 µs).
+// Kernel choice by workgroup count (one per query tile and head group), measured on one box at
+// hq 32 / hkv 8: up to two per CU the two-group kernel, which splits each tile's keys over two
+// wave groups (T = 2048: 512 workgroups, 58 vs 63 µs for the others; T = 512 at pos0 16384: 128
+// workgroups, 269 vs 358 µs); from three per CU the 32-key-stage kernel with three workgroups per
+// CU (T = 4096: 156 vs 187 µs; T = 8192: 580 vs 631 µs); in between the four-wave kernel
+// (T = 2560: 76 vs 82 µs). BRASA_PREFILL_VARIANT=1, 2 or 4 forces one of them.
 template <int HW, bool PS>
 int launch_f16(const PrefillArgs& a, hipStream_t stream) {
     const long long wgs = (long long)(a.hq / HW) * a.ntiles;
-    if (wgs <= 2 * 256) {
+    static const int variant = getenv("BRASA_PREFILL_VARIANT") ? atoi(getenv("BRASA_PREFILL_VARIANT")) : 0;
+    const int pick = variant ? variant : wgs <= 2 * 256 ? 1 : wgs < 3 * 256 ? 2 : 4;
+    if (pick == 1) {
         hipLaunchKernelGGL((prefill_f16_kernel<HW, PS>), dim3(a.hq / HW, a.ntiles),
                            dim3(2 * kThreads), 0, stream, a);
         return check_launch("prefill_f16_kernel");
+    }
+    if (pick == 4) {
+        hipLaunchKernelGGL((prefill_f16_kernel4s<HW, PS>), dim3(a.hq / HW, a.ntiles), dim3(kThreads),
+                           0, stream, a);
+        return check_launch("prefill_f16_kernel4s");
     }
     hipLaunchKernelGGL((prefill_f16_kernel4<HW, PS>), dim3(a.hq / HW, a.ntiles), dim3(kThreads), 0,
                        stream, a);
