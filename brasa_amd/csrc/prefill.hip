@@ -836,11 +836,12 @@ prefill_f16_kernel4(PrefillArgs a) {
     }
 }
 
-// Three workgroups per CU: prefill_f16_kernel4's tile code on 32-key stages (32 KB of LDS per
-// workgroup) with the per-lane operand offsets recomputed at each use, so a wave fits 168
-// registers and each SIMD holds three waves. The kernel is latency-bound (matrix cores ~27 %
-// busy, LDS ~15 %): a third wave per SIMD hides more of the dependent chains. Query tiles
-// heaviest first; the dispatcher hands the light ones to CUs as they free up.
+// Three workgroups per CU: prefill_f16_kernel4's tile code on 32-key stages in a three-stage
+// ring (48 KB of LDS per workgroup), with the per-lane operand offsets recomputed at each use so
+// a wave fits 168 registers and each SIMD holds three waves. The kernel is latency-bound (matrix
+// cores ~27 % busy, LDS ~15 %): a third wave per SIMD and two stages in flight hide more of the
+// dependent chains and of the copies' latency. Query tiles heaviest first; the dispatcher hands
+// the light ones to CUs as they free up.
 constexpr int kTileS = 32;                    // keys per stage
 constexpr int kStageHalvesS = kTileS * kDim;  // one 32 x 128 f16 tile
 template <int HW, bool PS>
@@ -848,8 +849,9 @@ __global__ void __launch_bounds__(kThreads, 3)
 prefill_f16_kernel4s(PrefillArgs a) {
     constexpr int TPW = 32 * 4 / HW;
     constexpr int kTileBytes = kStageHalvesS * 2;
-    __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kStageHalvesS];
-    __shared__ __attribute__((aligned(16))) uint16_t s_vv[2][kStageHalvesS];
+    // three-stage ring: the copies of stage i + 2 are issued when stage i starts (48 KB)
+    __shared__ __attribute__((aligned(16))) uint16_t s_k[3][kStageHalvesS];
+    __shared__ __attribute__((aligned(16))) uint16_t s_vv[3][kStageHalvesS];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -977,26 +979,31 @@ prefill_f16_kernel4s(PrefillArgs a) {
         }
     };
 
-    // stages alternate between the two LDS buffers; stage i + 1 streams in during stage i.
-    // Stage 0's copies go out right behind the Q loads, then the Q conversion.
+    // stage i sits in ring slot i % 3; the copies of stage i + 2 go out when stage i starts, so
+    // two stages stream in while one is contracted. Stages 0 and 1 go out right behind the Q
+    // loads, then the Q conversion.
     dma(0, 0);
+    if (kTileS < kend_wg) dma(kTileS, 1);
     q_convert(qraw, a.scale, qvalid, qh);
-    for (int kb = 0; kb < kend_wg; kb += 2 * kTileS) {
+    for (int kb = 0; kb < kend_wg; kb += 3 * kTileS) {
 #pragma unroll
-        for (int half_i = 0; half_i < 2; ++half_i) {
-            const int kbi = kb + half_i * kTileS;
+        for (int r = 0; r < 3; ++r) {
+            const int kbi = kb + r * kTileS;
             if (kbi >= kend_wg) break;
-            __syncthreads();  // every wave is done with the buffer the next copy overwrites
-            if (kbi + kTileS < kend_wg) {
-                dma(kbi + kTileS, half_i ^ 1);
+            __syncthreads();  // every wave is done with the slot the next copy overwrites
+            if (kbi + 2 * kTileS < kend_wg) {
+                dma(kbi + 2 * kTileS, (r + 2) % 3);
+                wait_vmcnt<8>();
+            } else if (kbi + kTileS < kend_wg) {
                 wait_vmcnt<4>();
             } else {
                 wait_vmcnt<0>();
             }
             __syncthreads();
             if (kbi < kend_w) {
-                if (half_i == 0) stage(kbi, std::integral_constant<int, 0>{});
-                else stage(kbi, std::integral_constant<int, 1>{});
+                if (r == 0) stage(kbi, std::integral_constant<int, 0>{});
+                else if (r == 1) stage(kbi, std::integral_constant<int, 1>{});
+                else stage(kbi, std::integral_constant<int, 2>{});
             }
         }
     }
