@@ -136,3 +136,29 @@ def test_flash_four_wave_variant():
               f"F16_PF32 worst_f16 {w:.2e}")
         assert a <= 2e-3 and r <= 1e-2, (t0, a, r)
         assert w <= 1e-5, (t0, w)
+
+
+def test_flash_stage_ring_variant():
+    # 128 query heads (group 4) x 25 tiles of 32 tokens = 800 workgroups, three or more per CU:
+    # the F16 precisions run the 32-key-stage kernel. Rows of the first, a middle and the last
+    # tiles are checked.
+    k = Kernels()
+    rng = oracle.Rng(43)
+    tokens, pos0, hq, hkv = 800, 21, 128, 32
+    lk = pos0 + tokens
+    cap = (lk + 63) // 64 * 64
+    q = rng.vec(tokens * hq * DIM, 2.0)
+    cache = KvPair(KvType.F16, rng.vec(cap * hkv * DIM, 2.0), rng.vec(cap * hkv * DIM, 3.0))
+    _say(f"prefill stage-ring F16 hq={hq} T={tokens} pos0={pos0}")
+    oh = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
+    _say(f"prefill stage-ring F16_PF32 hq={hq} T={tokens} pos0={pos0}")
+    op = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16_PF32)
+    for t0, t1 in [(0, 24), (390, 414), (776, 800)]:
+        ref16, vmax = oracle.attention(q, cache.k, cache.v, tokens, hq, hkv, DIM, pos0,
+                                       q16=True, rows=(t0, t1))
+        a, r = bars(oracle.f16_to_f32(oh[t0:t1]), ref16[t0:t1])
+        w = oracle.worst_f16(op[t0:t1], ref16[t0:t1], vmax[t0:t1])
+        print(f"stage-ring rows {t0}:{t1}: F16 max-abs {a:.2e} max-rel {r:.2e}; "
+              f"F16_PF32 worst_f16 {w:.2e}")
+        assert a <= 2e-3 and r <= 1e-2, (t0, a, r)
+        assert w <= 1e-5, (t0, w)
