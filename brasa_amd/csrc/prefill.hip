@@ -46,6 +46,7 @@ struct PrefillArgs {
     void* o;
     int tokens, hq, hkv, group, pos0;
     int ntiles;                 // query tiles
+    int pair;                   // prefill_f16_kernel: workgroup y runs tiles ntiles - 1 - y and y
     float scale;
 };
 
@@ -344,14 +345,15 @@ constexpr int kStageHalves = kTile * kDim;  // one 64 x 128 f16 tile
 __device__ __forceinline__ int kswz(int r, int c) { return c ^ (r & 15); }
 __device__ __forceinline__ int vswz(int r, int c) { return c ^ (4 * (r & 3)); }
 
+// One query tile of prefill_f16_kernel (the workgroup's whole work for it, merge and store
+// included); s_kv = [K / V][group][buffer]: each group streams its own 64-key tiles; K and V
+// have their own double buffers because K of tile i is free after tile i's QK^T, V only after
+// its PV.
 template <int HW, bool PS>
-__global__ void __launch_bounds__(2 * kThreads, 1)
-prefill_f16_kernel(PrefillArgs a) {
+__device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile,
+                                            uint16_t (&s_kv)[2][2][2][kStageHalves]) {
     constexpr int TPW = 32 * 4 / HW;
     constexpr int kTileBytes = kStageHalves * 2;
-    // [K / V][group][buffer]: each group streams its own 64-key tiles; K and V have their own
-    // double buffers because K of tile i is free after tile i's QK^T, V only after its PV
-    __shared__ __attribute__((aligned(16))) uint16_t s_kv[2][2][2][kStageHalves];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -360,10 +362,7 @@ prefill_f16_kernel(PrefillArgs a) {
     const int col = lane & 31;
     const int u = lane >> 5;
 
-    // Work order: head groups fastest (they spread over the XCDs), query tiles heaviest first
-    // (one workgroup per CU; a CU that finishes a light tile early takes the next one).
     const int hg = blockIdx.x;
-    const int tile = a.ntiles - 1 - (int)blockIdx.y;
     const int h = hg * HW + (qw % HW);
     const int kh = (hg * HW) / a.group;
     const int t0 = tile * TPW;
@@ -600,7 +599,12 @@ prefill_f16_kernel(PrefillArgs a) {
         xch[65] = lsum;
     }
     __syncthreads();
-    if (grp == 1) return;
+    // the last barrier of the tile: after it the exchange area (the LDS of the next tile's
+    // copies) has been read
+    if (grp == 1) {
+        __syncthreads();
+        return;
+    }
     {
         const float mb2 = xch[64], lb = xch[65];
         const float M = fmaxf(m_used, mb2);
@@ -613,6 +617,7 @@ prefill_f16_kernel(PrefillArgs a) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[dt][i] = acc[dt][i] * wa + xch[16 * dt + i] * wb;
     }
+    __syncthreads();
 
     const float L = lsum + __shfl_xor(lsum, 32, 64);
     if (!qvalid) return;
@@ -631,6 +636,20 @@ prefill_f16_kernel(PrefillArgs a) {
             *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.o) + obase + d) = w;
         }
     }
+}
+
+// Work order: head groups fastest (they spread over the XCDs), query tiles heaviest first. With
+// a.pair the workgroup for y also takes the light tile y after the heavy tile ntiles - 1 - y, so
+// each CU receives a pair of equal total work in one round (without it, a CU that finishes a
+// light tile early takes the next one).
+template <int HW, bool PS>
+__global__ void __launch_bounds__(2 * kThreads, 1)
+prefill_f16_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t s_kv[2][2][2][kStageHalves];
+    const int y = blockIdx.y;
+    const int heavy = a.ntiles - 1 - y;
+    f16_pp_tile<HW, PS>(a, heavy, s_kv);
+    if (a.pair && y < heavy) f16_pp_tile<HW, PS>(a, y, s_kv);
 }
 
 // Four-wave variant (one group, no key split), two workgroups per CU: with many query tiles per
@@ -1039,15 +1058,24 @@ int launch(const PrefillArgs& a, hipStream_t stream) {
 // wave groups (T = 2048: 512 workgroups, 58 vs 63 µs for the others; T = 512 at pos0 16384: 128
 // workgroups, 269 vs 358 µs); from three per CU the 32-key-stage kernel with three workgroups per
 // CU (T = 4096: 156 vs 187 µs; T = 8192: 580 vs 631 µs); in between the four-wave kernel
-// (T = 2560: 76 vs 82 µs). BRASA_PREFILL_VARIANT=1, 2 or 4 forces one of them.
+// (T = 2560: 76 vs 82 µs). BRASA_PREFILL_VARIANT=1, 2 or 4 forces one of them. The two-group
+// kernel pairs heavy and light query tiles when the pairs still fill every CU (T = 2048:
+// 57.0 vs 58.6 µs; at T = 1536 the 192 pairs leave CUs idle, 44 vs 39 µs);
+// BRASA_PREFILL_PAIR=0 turns pairing off.
 template <int HW, bool PS>
 int launch_f16(const PrefillArgs& a, hipStream_t stream) {
     const long long wgs = (long long)(a.hq / HW) * a.ntiles;
-    static const int variant = getenv("BRASA_PREFILL_VARIANT") ? atoi(getenv("BRASA_PREFILL_VARIANT")) : 0;
+    const char* ev = getenv("BRASA_PREFILL_VARIANT");  // read per call (tests switch it)
+    const int variant = ev ? atoi(ev) : 0;
     const int pick = variant ? variant : wgs <= 2 * 256 ? 1 : wgs < 3 * 256 ? 2 : 4;
     if (pick == 1) {
-        hipLaunchKernelGGL((prefill_f16_kernel<HW, PS>), dim3(a.hq / HW, a.ntiles),
-                           dim3(2 * kThreads), 0, stream, a);
+        const char* ep = getenv("BRASA_PREFILL_PAIR");
+        const int pair_env = ep ? atoi(ep) : 1;
+        PrefillArgs b = a;
+        b.pair = pair_env && wgs >= 2 * 256;  // pairs still fill every CU
+        const int rows = b.pair ? (a.ntiles + 1) / 2 : a.ntiles;
+        hipLaunchKernelGGL((prefill_f16_kernel<HW, PS>), dim3(a.hq / HW, rows),
+                           dim3(2 * kThreads), 0, stream, b);
         return check_launch("prefill_f16_kernel");
     }
     if (pick == 4) {
@@ -1100,6 +1128,7 @@ int prefill_launch(const float* q, const void* k, const void* v, void* o, int to
     a.group = hq / hkv;
     a.pos0 = pos0;
     a.ntiles = 0;
+    a.pair = 0;
     a.scale = 1.0f / sqrtf(static_cast<float>(kDim));
     switch (kv) {
         case BRASA_KV_F32: return launch_kv<BRASA_KV_F32>(a, precision, stream);

@@ -162,3 +162,35 @@ def test_flash_stage_ring_variant():
               f"F16_PF32 worst_f16 {w:.2e}")
         assert a <= 2e-3 and r <= 1e-2, (t0, a, r)
         assert w <= 1e-5, (t0, w)
+
+
+def test_flash_paired_tiles(monkeypatch):
+    # 64 query heads (group 4) x 33 tiles of 32 tokens = 528 workgroups with the two-group
+    # kernel forced: heavy and light tiles run in pairs (y, 32 - y) and the middle tile 16 alone.
+    # The rows checked cover a heavy tile, the unpaired middle tile and a light tile; the same
+    # launch without pairing must give identical bits.
+    k = Kernels()
+    rng = oracle.Rng(47)
+    tokens, pos0, hq, hkv = 1040, 19, 64, 16
+    lk = pos0 + tokens
+    cap = (lk + 63) // 64 * 64
+    q = rng.vec(tokens * hq * DIM, 2.0)
+    cache = KvPair(KvType.F16, rng.vec(cap * hkv * DIM, 2.0), rng.vec(cap * hkv * DIM, 3.0))
+    monkeypatch.setenv("BRASA_PREFILL_VARIANT", "1")
+    _say(f"prefill paired F16 hq={hq} T={tokens} pos0={pos0}")
+    oh = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
+    _say(f"prefill paired F16_PF32 hq={hq} T={tokens} pos0={pos0}")
+    op = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16_PF32)
+    monkeypatch.setenv("BRASA_PREFILL_PAIR", "0")
+    _say(f"prefill unpaired F16 hq={hq} T={tokens} pos0={pos0}")
+    ou = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
+    assert np.array_equal(oh, ou)
+    for t0, t1 in [(0, 32), (512, 544), (1024, 1040)]:
+        ref16, vmax = oracle.attention(q, cache.k, cache.v, tokens, hq, hkv, DIM, pos0,
+                                       q16=True, rows=(t0, t1))
+        a, r = bars(oracle.f16_to_f32(oh[t0:t1]), ref16[t0:t1])
+        w = oracle.worst_f16(op[t0:t1], ref16[t0:t1], vmax[t0:t1])
+        print(f"paired rows {t0}:{t1}: F16 max-abs {a:.2e} max-rel {r:.2e}; "
+              f"F16_PF32 worst_f16 {w:.2e}")
+        assert a <= 2e-3 and r <= 1e-2, (t0, a, r)
+        assert w <= 1e-5, (t0, w)
