@@ -412,19 +412,23 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
     const uint32_t lds_v = lds_addr(&s_kv[1][grp][0][0]) + qw * 16 * 256;
     // tile i of this group = workgroup tile 2 i + grp, keys [kb(i), kb(i) + 64)
     auto kb_of = [&](int i) { return (2 * i + grp) * kTile; };
+    // lane-constant copy sources, computed once (8 registers; the copies are issued in the
+    // softmax phase, whose VALU slots are the less loaded ones)
+    uint32_t kso[4], vso[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        kso[r] = kdo(r, lrow, lchunk);
+        vso[r] = vdo(r, lrow, lchunk);
+    }
     auto dma_k = [&](int i) {
         const uint8_t* g = kbase + (size_t)kb_of(i) * rstride;
-        int lr = lrow, lc = lchunk;
-        asm volatile("" : "+v"(lr), "+v"(lc));  // recomputed per use (see koff)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) lds_dma16_s(g, kdo(r, lr, lc), lds_k + (i & 1) * kTileBytes + r * 1024);
+        for (int r = 0; r < 4; ++r) lds_dma16_s(g, kso[r], lds_k + (i & 1) * kTileBytes + r * 1024);
     };
     auto dma_v = [&](int i) {
         const uint8_t* g = vbase + (size_t)kb_of(i) * rstride;
-        int lr = lrow, lc = lchunk;
-        asm volatile("" : "+v"(lr), "+v"(lc));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) lds_dma16_s(g, vdo(r, lr, lc), lds_v + (i & 1) * kTileBytes + r * 1024);
+        for (int r = 0; r < 4; ++r) lds_dma16_s(g, vso[r], lds_v + (i & 1) * kTileBytes + r * 1024);
     };
 
     f32x16 acc[4];
@@ -577,11 +581,11 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
         const bool on = k <= ng;
         if (on) wait_for(k);
         __syncthreads();
-        if (on) {
-            mphase(k);
-            copies_after(k);
-        }
+        if (on) mphase(k);
         __syncthreads();
+        // after the barrier every wave of the group has read K(k) and V(k - 1): their buffers
+        // take K(k + 2) and V(k + 1)
+        if (on) copies_after(k);
         if (k < ng) vphase(k);
     }
     if (grp == 0) __syncthreads();
