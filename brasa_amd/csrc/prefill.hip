@@ -916,16 +916,21 @@ prefill_f16_kernel4s(PrefillArgs a) {
     // each wave copies 8 rows of a 32-key stage: rows 8 wave + 4 r + lane / 16
     const uint32_t lds_k = lds_addr(&s_k[0][0]) + wave * 8 * 256;
     const uint32_t lds_v = lds_addr(&s_vv[0][0]) + wave * 8 * 256;
+    // lane-constant copy sources, computed once (4 registers instead of a 32-bit multiply per copy)
+    uint32_t kso[2], vso[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int row = 8 * wave + 4 * r + (lane >> 4), lc = lane & 15;
+        kso[r] = (uint32_t)(row * rstride + 16 * kswz(row, lc));
+        vso[r] = (uint32_t)(row * rstride + 16 * vswz(row, lc));
+    }
     auto dma = [&](int kb, int buf) {
         const uint8_t* kg = kbase + (size_t)kb * rstride;
         const uint8_t* vg = vbase + (size_t)kb * rstride;
-        int lr = lane >> 4, lc = lane & 15;
-        asm volatile("" : "+v"(lr), "+v"(lc));  // recomputed per use
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
-            const int row = 8 * wave + 4 * r + lr;
-            lds_dma16_s(kg, (uint32_t)(row * rstride + 16 * kswz(row, lc)), lds_k + buf * kTileBytes + r * 1024);
-            lds_dma16_s(vg, (uint32_t)(row * rstride + 16 * vswz(row, lc)), lds_v + buf * kTileBytes + r * 1024);
+            lds_dma16_s(kg, kso[r], lds_k + buf * kTileBytes + r * 1024);
+            lds_dma16_s(vg, vso[r], lds_v + buf * kTileBytes + r * 1024);
         }
     };
 
