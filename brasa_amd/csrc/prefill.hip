@@ -112,6 +112,34 @@ __device__ __forceinline__ void q_convert(const u32x4 (&raw)[16], float scale, b
     }
 }
 
+// Half of a Q row for the two-group kernel: group g loads and converts the k-steps 4 g .. 4 g + 3
+// (head dims 64 g .. 64 g + 63) of its column, the other group the rest, and the halves meet in
+// LDS: each row is read from HBM once per workgroup instead of once per group.
+__device__ __forceinline__ void q_load_half(const float* qrow, int u, int g, u32x4 (&raw)[8]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            raw[2 * j + h] = *reinterpret_cast<const u32x4*>(qrow + 16 * (4 * g + j) + 8 * u + 4 * h);
+    __builtin_amdgcn_sched_barrier(0);
+}
+__device__ __forceinline__ void q_convert_half(const u32x4 (&raw)[8], float scale, bool valid,
+                                               half8 (&qh)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const f32x4 x0 = __builtin_bit_cast(f32x4, raw[2 * j]);
+        const f32x4 x1 = __builtin_bit_cast(f32x4, raw[2 * j + 1]);
+        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        uint16_t hi[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float sx = as_f32(xs[i] * scale);  // f32 product, then f16
+            hi[i] = f2h(valid ? sx : 0.0f);
+        }
+        qh[j] = pack8(hi);
+    }
+}
+
 // KV = cache type; HW = query heads per workgroup (1, 2, 4); QS = split Q (F32 precision);
 // PS = split P; OF32 = f32 output.
 template <int KV, int HW, bool QS, bool PS, bool OF32>
@@ -375,8 +403,8 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
     const int tq = tw0 + col;
     const bool qvalid = tq < a.tokens;
     half8 qh[8];
-    u32x4 qraw[16];
-    q_load(a.q + ((size_t)(qvalid ? tq : 0) * a.hq + h) * kDim, u, qraw);
+    u32x4 qraw[8];
+    q_load_half(a.q + ((size_t)(qvalid ? tq : 0) * a.hq + h) * kDim, u, grp, qraw);
 
     // lane-constant byte offsets: K operand rows (per k-step t), V^T tr16 sources (per dt),
     // DMA sources (per row quad r)
@@ -566,11 +594,26 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
         else wait_vmcnt<0>();
     };
 
-    // prologue: K(0), K(1), V(0) right behind the Q loads, then the Q conversion
+    // prologue: K(0), K(1), V(0) right behind the Q loads, then the Q conversion; the two
+    // halves of each Q operand meet in group g's V buffer 1, idle until V(1) is copied after
+    // MFMA phase 0 (every wave has read its Q by then: the barriers before that copy wait for
+    // outstanding LDS reads)
     if (0 < ng) dma_k(0);
     if (1 < ng) dma_k(1);
     if (0 < ng) dma_v(0);
-    q_convert(qraw, a.scale, qvalid, qh);
+    {
+        half8 qpart[4];
+        q_convert_half(qraw, a.scale, qvalid, qpart);
+        uint8_t* qx = reinterpret_cast<uint8_t*>(&s_kv[1][grp][1][0]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<uint4*>(qx + ((qw * 4 + j) * 64 + lane) * 16) = __builtin_bit_cast(uint4, qpart[j]);
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            qh[t] = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(
+                reinterpret_cast<const uint8_t*>(&s_kv[1][t >> 2][1][0]) + ((qw * 4 + (t & 3)) * 64 + lane) * 16));
+    }
     // Both groups run the same loop (MFMA phase k, barrier, softmax phase k, barrier); group 1
     // passes one extra barrier before it and group 0 one after it, so the barrier counts match
     // while group 1 runs one phase behind: each group's MFMA phase overlaps the other group's
