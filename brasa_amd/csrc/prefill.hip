@@ -667,21 +667,33 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
     __syncthreads();
 
     const float L = lsum + __shfl_xor(lsum, 32, 64);
-    if (!qvalid) return;
-    const float inv = 1.0f / L;
-    const size_t obase = ((size_t)tq * a.hq + h) * kDim;
+    const float inv = 1.0f / L;  // padding columns: never stored
+    // The 32 x 128 f16 output tile goes row-major through this wave's 8 KB of group 0's K
+    // buffers (group 0 copies into them only after this epilogue; group 1, possibly in its next
+    // tile already, uses its own buffers), 16-byte chunk c of row r at chunk c ^ (r & 15), so
+    // each store below writes 4 whole 256-byte rows instead of 16 bytes of 32 rows.
+    uint8_t* ot = reinterpret_cast<uint8_t*>(&s_kv[0][0][0][0]) + qw * 32 * 256;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const int d = 32 * dt + 8 * g + 4 * u;
             uint2 w;
             w.x = (uint32_t)f2h(as_f32(acc[dt][4 * g] * inv)) |
                   ((uint32_t)f2h(as_f32(acc[dt][4 * g + 1] * inv)) << 16);
             w.y = (uint32_t)f2h(as_f32(acc[dt][4 * g + 2] * inv)) |
                   ((uint32_t)f2h(as_f32(acc[dt][4 * g + 3] * inv)) << 16);
-            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.o) + obase + d) = w;
+            *reinterpret_cast<uint2*>(ot + col * 256 + 16 * ((4 * dt + g) ^ (col & 15)) + 8 * u) = w;
         }
+    }
+    asm volatile("" ::: "memory");  // a wave's LDS accesses execute in order
+    const int rq = lane >> 4, cq = lane & 15;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int row = 4 * i + rq;
+        const uint4 v = *reinterpret_cast<const uint4*>(ot + row * 256 + 16 * (cq ^ (row & 15)));
+        if (tw0 + row < a.tokens)
+            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.o) +
+                                      ((size_t)(tw0 + row) * a.hq + h) * kDim + 8 * cq) = v;
     }
 }
 
