@@ -112,6 +112,36 @@ __device__ __forceinline__ void q_convert(const u32x4 (&raw)[16], float scale, b
     }
 }
 
+// Output of one f16-kernel wave: its 32 x 128 tile (accumulator layout, times inv) rounded to f16
+// and written row-major into 8 KB of LDS at ot (16-byte chunk c of row r at chunk c ^ (r & 15),
+// conflict-free both ways), then stored 4 whole 256-byte rows per instruction (instead of 16
+// bytes of each of 32 rows). Rows tw0 + r at or past tokens are not stored.
+__device__ __forceinline__ void store_o_rows(const f32x16 (&acc)[4], float inv, uint8_t* ot,
+                                             int lane, void* o, int tw0, int tokens, int hq, int h) {
+    const int col = lane & 31, u = lane >> 5;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            uint2 w;
+            w.x = (uint32_t)f2h(as_f32(acc[dt][4 * g] * inv)) |
+                  ((uint32_t)f2h(as_f32(acc[dt][4 * g + 1] * inv)) << 16);
+            w.y = (uint32_t)f2h(as_f32(acc[dt][4 * g + 2] * inv)) |
+                  ((uint32_t)f2h(as_f32(acc[dt][4 * g + 3] * inv)) << 16);
+            *reinterpret_cast<uint2*>(ot + col * 256 + 16 * ((4 * dt + g) ^ (col & 15)) + 8 * u) = w;
+        }
+    }
+    asm volatile("" ::: "memory");  // a wave's LDS accesses execute in order
+    const int rq = lane >> 4, cq = lane & 15;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int row = 4 * i + rq;
+        const uint4 v = *reinterpret_cast<const uint4*>(ot + row * 256 + 16 * (cq ^ (row & 15)));
+        if (tw0 + row < tokens)
+            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(o) + ((size_t)(tw0 + row) * hq + h) * kDim + 8 * cq) = v;
+    }
+}
+
 // Half of a Q row for the two-group kernel: group g loads and converts the k-steps 4 g .. 4 g + 3
 // (head dims 64 g .. 64 g + 63) of its column, the other group the rest, and the halves meet in
 // LDS: each row is read from HBM once per workgroup instead of once per group.
@@ -668,33 +698,10 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
 
     const float L = lsum + __shfl_xor(lsum, 32, 64);
     const float inv = 1.0f / L;  // padding columns: never stored
-    // The 32 x 128 f16 output tile goes row-major through this wave's 8 KB of group 0's K
-    // buffers (group 0 copies into them only after this epilogue; group 1, possibly in its next
-    // tile already, uses its own buffers), 16-byte chunk c of row r at chunk c ^ (r & 15), so
-    // each store below writes 4 whole 256-byte rows instead of 16 bytes of 32 rows.
-    uint8_t* ot = reinterpret_cast<uint8_t*>(&s_kv[0][0][0][0]) + qw * 32 * 256;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            uint2 w;
-            w.x = (uint32_t)f2h(as_f32(acc[dt][4 * g] * inv)) |
-                  ((uint32_t)f2h(as_f32(acc[dt][4 * g + 1] * inv)) << 16);
-            w.y = (uint32_t)f2h(as_f32(acc[dt][4 * g + 2] * inv)) |
-                  ((uint32_t)f2h(as_f32(acc[dt][4 * g + 3] * inv)) << 16);
-            *reinterpret_cast<uint2*>(ot + col * 256 + 16 * ((4 * dt + g) ^ (col & 15)) + 8 * u) = w;
-        }
-    }
-    asm volatile("" ::: "memory");  // a wave's LDS accesses execute in order
-    const int rq = lane >> 4, cq = lane & 15;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int row = 4 * i + rq;
-        const uint4 v = *reinterpret_cast<const uint4*>(ot + row * 256 + 16 * (cq ^ (row & 15)));
-        if (tw0 + row < a.tokens)
-            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.o) +
-                                      ((size_t)(tw0 + row) * a.hq + h) * kDim + 8 * cq) = v;
-    }
+    // this wave's 8 KB of group 0's K buffers: group 0 copies into them only after this
+    // epilogue; group 1, possibly in its next tile already, uses its own buffers
+    store_o_rows(acc, inv, reinterpret_cast<uint8_t*>(&s_kv[0][0][0][0]) + qw * 32 * 256, lane, a.o,
+                 tw0, a.tokens, a.hq, h);
 }
 
 // Work order: head groups fastest (they spread over the XCDs), query tiles heaviest first. With
@@ -896,22 +903,10 @@ prefill_f16_kernel4(PrefillArgs a) {
     }
 
     const float L = lsum + __shfl_xor(lsum, 32, 64);
-    if (!qvalid) return;
-    const float inv = 1.0f / L;
-    const size_t obase = ((size_t)tq * a.hq + h) * kDim;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int d = 32 * dt + 8 * g + 4 * u;
-            uint2 w;
-            w.x = (uint32_t)f2h(as_f32(acc[dt][4 * g] * inv)) |
-                  ((uint32_t)f2h(as_f32(acc[dt][4 * g + 1] * inv)) << 16);
-            w.y = (uint32_t)f2h(as_f32(acc[dt][4 * g + 2] * inv)) |
-                  ((uint32_t)f2h(as_f32(acc[dt][4 * g + 3] * inv)) << 16);
-            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.o) + obase + d) = w;
-        }
-    }
+    const float inv = 1.0f / L;  // padding columns: never stored
+    __syncthreads();  // every wave is done with the K stages: wave w stages its output in 8 KB of them
+    store_o_rows(acc, inv, reinterpret_cast<uint8_t*>(&s_k[0][0]) + wave * 32 * 256, lane, a.o, tw0,
+                 a.tokens, a.hq, h);
 }
 
 // Three workgroups per CU: prefill_f16_kernel4's tile code on 32-key stages in a three-stage
@@ -1092,22 +1087,11 @@ prefill_f16_kernel4s(PrefillArgs a) {
     }
 
     const float L = lsum + __shfl_xor(lsum, 32, 64);
-    if (!qvalid) return;
-    const float inv = 1.0f / L;
-    const size_t obase = ((size_t)tq * a.hq + h) * kDim;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int d = 32 * dt + 8 * g + 4 * u;
-            uint2 w;
-            w.x = (uint32_t)f2h(as_f32(acc[dt][4 * g] * inv)) |
-                  ((uint32_t)f2h(as_f32(acc[dt][4 * g + 1] * inv)) << 16);
-            w.y = (uint32_t)f2h(as_f32(acc[dt][4 * g + 2] * inv)) |
-                  ((uint32_t)f2h(as_f32(acc[dt][4 * g + 3] * inv)) << 16);
-            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.o) + obase + d) = w;
-        }
-    }
+    const float inv = 1.0f / L;  // padding columns: never stored
+    __syncthreads();  // every wave is done with the stages: waves 0-2 stage their output in the
+                      // three 8 KB K stages, wave 3 in V stage 0
+    store_o_rows(acc, inv, reinterpret_cast<uint8_t*>(wave < 3 ? &s_k[wave][0] : &s_vv[0][0]), lane,
+                 a.o, tw0, a.tokens, a.hq, h);
 }
 
 template <int KV, int HW, bool QS, bool PS, bool OF32>
