@@ -77,6 +77,16 @@ __device__ __forceinline__ half8 pack8(const uint16_t (&x)[8]) {
     return __builtin_bit_cast(half8, c);
 }
 
+// value combined with that of lane l ^ 32 (v_permlane32_swap: VALU, no LDS round trip)
+__device__ __forceinline__ float max_xor32(float x) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+    return fmaxf(__int_as_float(sw[0]), __int_as_float(sw[1]));
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+    return __int_as_float(sw[0]) + __int_as_float(sw[1]);
+}
+
 __device__ __forceinline__ f32x16 mfma(half8 a, half8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
@@ -318,7 +328,7 @@ prefill_kernel(PrefillArgs a) {
                 tmax = fmaxf(tmax, x);
             }
         }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        tmax = max_xor32(tmax);
         const float mn = fmaxf(m2, tmax);  // finite: key 0 is visible to every query
         const float alpha = __builtin_amdgcn_exp2f(m2 - mn);
         m2 = mn;
@@ -363,7 +373,7 @@ prefill_kernel(PrefillArgs a) {
     }
 
     // ---- normalise and write O[t, h, d] --------------------------------------------------
-    const float L = lsum + __shfl_xor(lsum, 32, 64);
+    const float L = sum_xor32(lsum);
     if (!qvalid) return;
     const float inv = 1.0f / L;
     const size_t obase = ((size_t)tq * a.hq + h) * kDim;
@@ -581,7 +591,7 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
         for (int b = 0; b < 2; ++b)
 #pragma unroll
             for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[b][r]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        tmax = max_xor32(tmax);
         const bool grow = tmax > m_used + kGrow;  // false while the column has no key
         if (__builtin_amdgcn_ballot_w64(grow)) {
             const float alpha = grow ? __builtin_amdgcn_exp2f((m_used - tmax) * kLog2e) : 1.0f;
@@ -696,7 +706,7 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
     }
     __syncthreads();
 
-    const float L = lsum + __shfl_xor(lsum, 32, 64);
+    const float L = sum_xor32(lsum);
     const float inv = 1.0f / L;  // padding columns: never stored
     // this wave's 8 KB of group 0's K buffers: group 0 copies into them only after this
     // epilogue; group 1, possibly in its next tile already, uses its own buffers
@@ -834,7 +844,7 @@ prefill_f16_kernel4(PrefillArgs a) {
                 for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[b][i]);
             }
         }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        tmax = max_xor32(tmax);
         const bool grow = tmax > m_used + kGrow;
         if (__builtin_amdgcn_ballot_w64(grow)) {
             const float alpha = grow ? __builtin_amdgcn_exp2f((m_used - tmax) * kLog2e) : 1.0f;
@@ -902,7 +912,7 @@ prefill_f16_kernel4(PrefillArgs a) {
         }
     }
 
-    const float L = lsum + __shfl_xor(lsum, 32, 64);
+    const float L = sum_xor32(lsum);
     const float inv = 1.0f / L;  // padding columns: never stored
     __syncthreads();  // every wave is done with the K stages: wave w stages its output in 8 KB of them
     store_o_rows(acc, inv, reinterpret_cast<uint8_t*>(&s_k[0][0]) + wave * 32 * 256, lane, a.o, tw0,
@@ -1016,10 +1026,7 @@ prefill_f16_kernel4s(PrefillArgs a) {
         float tmax = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
-        {
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(tmax), __float_as_int(tmax), false, false);
-            tmax = fmaxf(__int_as_float(sw[0]), __int_as_float(sw[1]));
-        }
+        tmax = max_xor32(tmax);
         const bool grow = tmax > m_used + kGrow;
         if (__builtin_amdgcn_ballot_w64(grow)) {
             const float alpha = grow ? __builtin_amdgcn_exp2f((m_used - tmax) * kLog2e) : 1.0f;
@@ -1086,7 +1093,7 @@ prefill_f16_kernel4s(PrefillArgs a) {
         }
     }
 
-    const float L = lsum + __shfl_xor(lsum, 32, 64);
+    const float L = sum_xor32(lsum);
     const float inv = 1.0f / L;  // padding columns: never stored
     __syncthreads();  // every wave is done with the stages: waves 0-2 stage their output in the
                       // three 8 KB K stages, wave 3 in V stage 0
