@@ -7,12 +7,16 @@
 // f64-computed cos/sin table, written back in place, and k (rotated) and v (as given) are stored
 // into the cache from pos0 on in the cache type (store_kv rounding: f16 RNE or q8_0).
 //
-// Design: one wave64 per 128-element row (lane l holds elements l and l + 64, which are exactly
-// a RoPE pair), four rows per workgroup. The sum of squares has one fixed order shared with the
-// unfused rms_norm kernel (lane partials in index order, then a xor butterfly 32, 16, .., 1), so
+// Design: lane l of a wave64 holds elements l and l + 64 of a 128-element row (exactly a RoPE
+// pair); each wave takes four consecutive rows and issues every load of the four (row, norm
+// weights, cos/sin) before the first reduction, so a wave keeps 4 rows of reads in flight (in-place
+// writes of one row could otherwise alias the next row's loads and serialise them). The sum of
+// squares has one fixed order shared with the unfused rms_norm kernel (lane partials in index
+// order, then a butterfly inside 16-lane rows by DPP and across rows by v_permlane16/32_swap), so
 // fused and unfused results are identical bits, as the reference's fused test demands
 // (crates/kernels/tests/fused.rs:8-98). The q8_0 groups of 32 are half-waves: the group amax is
-// five xor shuffles. HBM-bound: T * (hq + 2 hkv) * 512 B read, q/k rewritten, cache rows written.
+// the same exchanges without the last one. HBM-bound: T * (hq + 2 hkv) * 512 B read, q/k
+// rewritten, cache rows written.
 #include <cmath>
 #include <vector>
 
@@ -21,18 +25,28 @@
 namespace brasa {
 namespace {
 
-constexpr int kRowsPerWg = 4;
+constexpr int kRowsPerWg = 4;    // rms_norm: one row per wave
+constexpr int kWavesPerWg = 4;   // qk_norm_rope_store
+constexpr int kRowsPerWave = 4;
 
-// Sum over the wave of the per-lane partials, in the fixed xor-butterfly order.
+// Sum over the wave of the per-lane partials in one fixed order: the 16-lane DPP butterfly, then
+// lanes l ^ 16 and l ^ 32. Partners always add the same two values, so every lane ends with
+// identical bits.
 __device__ __forceinline__ float wave_sum(float p) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) p += __shfl_xor(p, m, 64);
-    return p;
+    p = row16_sum(p);
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_int(p), __float_as_int(p), false, false);
+    p = __int_as_float(a[0]) + __int_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_int(p), __float_as_int(p), false, false);
+    return __int_as_float(b[0]) + __int_as_float(b[1]);
 }
+// max over the 32 lanes of each half-wave
 __device__ __forceinline__ float half_wave_max(float x) {
-#pragma unroll
-    for (int m = 16; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m, 64));
-    return x;
+    x = fmaxf(x, dpp<0x140>(x));
+    x = fmaxf(x, dpp<0x141>(x));
+    x = fmaxf(x, dpp<0x1B>(x));
+    x = fmaxf(x, dpp<0xB1>(x));
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
+    return fmaxf(__int_as_float(a[0]), __int_as_float(a[1]));
 }
 // 1 / sqrt(ss / n + eps) with IEEE divides and square root (the reference's precise::sqrt).
 __device__ __forceinline__ float rms_scale(float ss, int n, float eps) {
@@ -114,38 +128,66 @@ struct QkvArgs {
 };
 
 // Row gr of T * (hq + 2 hkv): within a token, first the hq query heads, then the hkv key heads,
-// then the hkv value heads (the reference's order, qkv.metal:59-61).
+// then the hkv value heads (the reference's order, qkv.metal:59-61). Wave w takes rows
+// 4 w .. 4 w + 3.
 template <int KV>
-__global__ void __launch_bounds__(64 * kRowsPerWg) qk_norm_rope_store_kernel(QkvArgs a) {
-    const int gr = blockIdx.x * kRowsPerWg + (threadIdx.x >> 6);
+__global__ void __launch_bounds__(64 * kWavesPerWg) qk_norm_rope_store_kernel(QkvArgs a) {
+    const int gr0 = (blockIdx.x * kWavesPerWg + (threadIdx.x >> 6)) * kRowsPerWave;
     const int lane = threadIdx.x & 63;
-    if (gr >= a.rows) return;
+    if (gr0 >= a.rows) return;
     const int per_tok = a.hq + 2 * a.hkv;
-    const int t = gr / per_tok, r = gr % per_tok;
-    if (r >= a.hq + a.hkv) {
-        const size_t vh = (size_t)t * a.hkv + (r - a.hq - a.hkv);
-        const float* vr = a.v + vh * kDim;
-        store_row<KV>(a.vc, vh, lane, vr[lane], vr[lane + 64]);
-        return;
+    float x0[kRowsPerWave], x1[kRowsPerWave], w0[kRowsPerWave], w1[kRowsPerWave];
+    float c[kRowsPerWave], sn[kRowsPerWave];
+    float* dst[kRowsPerWave];
+    size_t crow[kRowsPerWave];
+    int kind[kRowsPerWave];  // 0 q, 1 k, 2 v, 3 past the last row
+    // every load of the four rows first
+#pragma unroll
+    for (int j = 0; j < kRowsPerWave; ++j) {
+        const int gr = gr0 + j;
+        kind[j] = 3;
+        if (gr >= a.rows) continue;
+        const int t = gr / per_tok, r = gr % per_tok;
+        if (r >= a.hq + a.hkv) {
+            kind[j] = 2;
+            crow[j] = (size_t)t * a.hkv + (r - a.hq - a.hkv);
+            const float* vr = a.v + crow[j] * kDim;
+            x0[j] = vr[lane];
+            x1[j] = vr[lane + 64];
+            continue;
+        }
+        const bool is_q = r < a.hq;
+        kind[j] = is_q ? 0 : 1;
+        crow[j] = is_q ? (size_t)t * a.hq + r : (size_t)t * a.hkv + (r - a.hq);
+        dst[j] = (is_q ? a.q : a.k) + crow[j] * kDim;
+        x0[j] = dst[j][lane];
+        x1[j] = dst[j][lane + 64];
+        const float* w = is_q ? a.qn : a.kn;
+        w0[j] = w[lane];
+        w1[j] = w[lane + 64];
+        const size_t tp = (size_t)(a.pos0 + t) * (kDim / 2) + lane;
+        c[j] = a.cos_t[tp];
+        sn[j] = a.sin_t[tp];
     }
-    const bool is_q = r < a.hq;
-    const size_t idx = is_q ? (size_t)t * a.hq + r : (size_t)t * a.hkv + (r - a.hq);
-    float* x = (is_q ? a.q : a.k) + idx * kDim;
-    const float* w = is_q ? a.qn : a.kn;
-    const float x0 = x[lane], x1 = x[lane + 64];
-    float p = 0.0f;
-    p += x0 * x0;
-    p += x1 * x1;
-    const float scale = rms_scale(wave_sum(p), kDim, a.eps);
-    const float a0 = (x0 * scale) * w[lane];
-    const float b0 = (x1 * scale) * w[lane + 64];
-    const size_t tp = (size_t)(a.pos0 + t) * (kDim / 2) + lane;
-    const float c = a.cos_t[tp], s = a.sin_t[tp];
-    const float y0 = a0 * c - b0 * s;
-    const float y1 = b0 * c + a0 * s;
-    x[lane] = y0;
-    x[lane + 64] = y1;
-    if (!is_q) store_row<KV>(a.kc, idx, lane, y0, y1);
+#pragma unroll
+    for (int j = 0; j < kRowsPerWave; ++j) {
+        if (kind[j] == 3) break;
+        if (kind[j] == 2) {
+            store_row<KV>(a.vc, crow[j], lane, x0[j], x1[j]);
+            continue;
+        }
+        float p = 0.0f;
+        p += x0[j] * x0[j];
+        p += x1[j] * x1[j];
+        const float scale = rms_scale(wave_sum(p), kDim, a.eps);
+        const float a0 = (x0[j] * scale) * w0[j];
+        const float b0 = (x1[j] * scale) * w1[j];
+        const float y0 = a0 * c[j] - b0 * sn[j];
+        const float y1 = b0 * c[j] + a0 * sn[j];
+        dst[j][lane] = y0;
+        dst[j][lane + 64] = y1;
+        if (kind[j] == 1) store_row<KV>(a.kc, crow[j], lane, y0, y1);
+    }
 }
 
 unsigned row_blocks(size_t rows) { return (unsigned)((rows + kRowsPerWg - 1) / kRowsPerWg); }
@@ -189,7 +231,8 @@ int qk_norm_rope_store_launch(int kv, float* q, float* k, const float* v, const 
     a.rows = (int)(tokens * (hq + 2 * hkv));
     a.eps = eps;
     if (a.rows == 0) return BRASA_OK;
-    const dim3 grid(row_blocks(a.rows)), block(64 * kRowsPerWg);
+    const int per_wg = kWavesPerWg * kRowsPerWave;
+    const dim3 grid((unsigned)((a.rows + per_wg - 1) / per_wg)), block(64 * kWavesPerWg);
     switch (kv) {
         case BRASA_KV_F32:
             hipLaunchKernelGGL(qk_norm_rope_store_kernel<BRASA_KV_F32>, grid, block, 0, stream, a);
