@@ -21,7 +21,11 @@
 //     spread over the 8 XCDs (each XCD's L2 keeps its head's K/V);
 //   * values that f16 cannot hold exactly (f32 and q8_0 caches, f32 Q, f32 P) are split as
 //     x = hi + lo with hi = f16(x), lo = f16(x - hi) and contracted with extra MFMAs
-//     (hi*hi + hi*lo + lo*hi), which keeps ~22 significant bits.
+//     (hi*hi + hi*lo + lo*hi), which keeps ~22 significant bits;
+//   * fp16 caches in the F16 / F16_PF32 precisions run one of three specialised kernels, picked
+//     by workgroup count: prefill_f16_kernel (8 waves, two key groups whose MFMA and softmax
+//     phases alternate; up to two workgroups per CU), prefill_f16_kernel4 (4 waves, two per CU)
+//     and prefill_f16_kernel4s (4 waves on 32-key stages, three per CU).
 #include <type_traits>
 
 #include "common.hpp"
