@@ -293,14 +293,21 @@ def profile_run(k: Kernels, stream: Stream, what: str) -> int:
     stream.synchronize()
     src.free()
     dst.free()
-    if what in ("decode", "decode_q8"):
-        layers = DecodeLayers(k, 16384, KvType.F16 if what == "decode" else KvType.Q8_0, stream)
+    decode_cases = {"decode": (16384, KvType.F16), "decode_q8": (16384, KvType.Q8_0),
+                    "decode_4k": (4096, KvType.F16), "decode_32k": (32768, KvType.F16)}
+    prefill_cases = {"prefill": (2048, 0), "prefill_8k": (8192, 0), "prefill_chunk": (512, 16384)}
+    if what in decode_cases:
+        lk, kv = decode_cases[what]
+        layers = DecodeLayers(k, lk, kv, stream)
         for _ in range(3):
             layers.step(stream)
         stream.synchronize()
         layers.free()
+    elif what == "decode_ragged":
+        bench_ragged(k, stream, 3, 1)
     else:
-        bench_prefill(k, stream, 2048, 0, KvType.F16, 10, 2)
+        tokens, pos0 = prefill_cases[what]
+        bench_prefill(k, stream, tokens, pos0, KvType.F16, 10, 2)
     log(f"profile run '{what}' done")
     return 0
 
@@ -312,7 +319,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="only the headline decode + 2K prefill")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--profile", choices=("decode", "decode_q8", "prefill"),
+    ap.add_argument("--profile", choices=("decode", "decode_q8", "decode_4k", "decode_32k",
+                                          "decode_ragged", "prefill", "prefill_8k",
+                                          "prefill_chunk"),
                     help="short fixed run for rocprofv3 (kernel trace / counters), no JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
