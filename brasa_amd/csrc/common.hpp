@@ -62,9 +62,6 @@ __device__ __forceinline__ float row16_sum(float x) {
     x += dpp<0xB1>(x);
     return x;
 }
-__device__ __forceinline__ float shfl_xor(float x, int mask) {
-    return __shfl_xor(x, mask, 64);
-}
 
 // ---- KV row access ------------------------------------------------------------------------
 // Cache element types, one per KvType value.
