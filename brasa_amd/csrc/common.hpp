@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
+#include <algorithm>
 #include <cstddef>
 #include <cstdint>
 #include <cstdlib>
@@ -20,6 +21,15 @@ constexpr float kLog2e = 1.4426950408889634f;
 // ---- host-side error plumbing -------------------------------------------------------------
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+
+// Decode launch plan (decode.hip): keys per split, splits of the longest sequence, and head
+// groups per workgroup.
+struct DecodePlan {
+    int chunk;
+    int splits;
+    int hpw;
+};
+DecodePlan decode_plan(const int* lk, int n, int ngroups, int G, int kv);
 
 // ---- f16 helpers --------------------------------------------------------------------------
 __device__ __forceinline__ float h2f(uint16_t h) {

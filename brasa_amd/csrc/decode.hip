@@ -3,27 +3,35 @@
 // Behaviour follows Kernels::decode_attention_lanes / decode_attention of the reference
 // (crates/kernels/src/lib.rs:1056-1164; decode_attention.metal:15-199): keys [0, lk) of one
 // layer cache are cut into splits; each split produces per query head the online-softmax
-// partial (m, l, acc[128]) and a second pass merges the splits as
-// o = sum_s w_s acc_s / sum_s w_s l_s with w_s = exp(m_s - max m).
+// partial (m, l, acc[128]) and the splits are merged as o = sum_s w_s acc_s / sum_s w_s l_s with
+// w_s = exp(m_s - max m) (attn_decode_reduce, decode_attention.metal:68-84).
 //
 // Design for MI355X (HBM-bound: every K/V byte is read once per GQA group):
-//   * workgroup = 4 wave64 = (split, KV head); a wave streams 32-key blocks of its split with the
-//     next block's K/V loads in flight while the current one is computed;
-//   * S^T = K Q^T on v_mfma_f32_16x16x32_f16. K rows go from HBM straight into the A operand
-//     (lane = key row, 8 contiguous dims: 16-byte loads, no conversion for f16 caches). The
-//     B operand holds the G query heads as columns, Q*scale split as hi + lo f16 (two MFMAs),
-//     so the scores keep f32 accuracy (the reference computes them in f32);
-//   * the S^T accumulator layout (lane = head column, 4 keys per lane) is used as the P^T
-//     B operand as it stands; P is split hi + lo as well. O^T += V^T P^T on the same MFMA, with
-//     V staged row-major in a wave-private LDS tile and read transposed by ds_read_tr16_b64;
-//   * online softmax in fp32 (exp2 domain) with two xor-shuffles per block for the row max;
-//   * the 4 waves merge through LDS into one partial per (head, split); a second small kernel
-//     merges the splits (an in-kernel "last workgroup merges" protocol was measured slower:
-//     its agent-scope release fence writes back the L2 of every workgroup's XCD);
+//   * workgroup = one head group (a KV head and its G query heads) x one split, W wave64 each
+//     streaming the split's 32-key blocks w, w + W, ... with the next block's K/V loads in
+//     flight. Workgroup b serves head group b % ngroups: with 8 KV heads the 8 XCDs each read
+//     one head (workgroups are dealt to the XCDs round robin), and a sequence needs only
+//     ~256 / ngroups splits, so the partials of a head group are few (32 at 16K keys);
+//   * S^T = K Q^T on v_mfma_f32_16x16x32_f16. K rows go from HBM straight into the A operand;
+//     the B operand holds the G query heads as columns, Q*scale split as hi + lo f16 so the
+//     scores keep f32 accuracy (the reference computes them in f32). The S^T accumulator
+//     layout is the P^T B operand as it stands; O^T += V^T P^T reads V transposed from LDS;
+//   * online softmax in fp32 (exp2 domain);
+//   * the split merge runs in the same kernel: the W waves merge through LDS, the workgroup
+//     stores its partial with device-coherent stores and counts itself in an arrival counter
+//     of its head group; the last workgroup to arrive merges all the splits and writes o. One
+//     kernel per call: a second dependent launch for the merge costs ~3 us per layer here;
 //   * q8_0: codes are exact in f16; K scales multiply the per-32-dim-group MFMA partials (one
 //     MFMA k-step is one group), V scales are folded into P per group; f32 caches are split
 //     hi + lo like Q.
+// A single-sequence call's result is a function of (q, k, v, lk) only: the split length and the
+// wave count per workgroup depend on lk alone (no tuning knob changes them) and every merge runs
+// in a fixed order. A batched launch shares one split length, taken from the batch's total keys,
+// so a sequence's splits, and with them the last bits of its result, can differ from the
+// single-sequence call (both within the decode tolerance).
+#include <atomic>
 #include <cstring>
+#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
@@ -35,26 +43,47 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4s lds_v4s;
 
-// Waves per workgroup: f16 caches use 8 (2 per SIMD, so one computes while the other's loads
-// are in flight); the register-staged q8_0 / f32 paths use 4 (LDS).
 constexpr int kBlock = 32;        // keys per wave iteration
-constexpr int kMaxWaves = 4;      // head groups per workgroup (one wave each)
 constexpr int kMinChunk = 128;    // keys per split >= DECODE_CHUNK keeps the scratch bound
 constexpr int kVStr = 144;        // V tile row stride in halves (256 B + 32 B pad)
-constexpr int kMaxSplits = 256;   // splits per sequence (the plan lengthens splits beyond that)
+constexpr int kTargetWgs = 256;   // workgroups per sequence the plan aims at (one per CU)
+
+// Waves per workgroup (fixed per cache type, so results never depend on the launch).
+constexpr int kWavesF16 = 8;
+constexpr int kWavesQ8 = 8;
+constexpr int kWavesF32 = 4;
+// Query heads of one merge group (a workgroup's HPW head groups) the final merge's thread layout
+// covers with 8 waves (kWavesF16 / kWavesQ8).
+constexpr int kMaxMergeHeads = 16;
+// Merge size bounds of the plan, in (query heads x splits) of a merge group; the last workgroup
+// loads 520 bytes per (query head, split). Up to kMergeWorkSmall (66 KB) for any layout; up to
+// kMergeWorkLong (~200 KB) when splits are long (>= kLongChunk keys), where streaming several KV
+// heads per workgroup gains more than the larger merge costs.
+constexpr int kMergeWorkSmall = 128;
+constexpr int kMergeWorkLong = 384;
+constexpr int kLongChunk = 512;
 
 // Sequences per launch: their descriptors travel in the kernel arguments (no device-side
 // metadata, so a call allocates and copies nothing).
 constexpr int kMaxSeqs = 64;
+
+// Arrival counters of the in-kernel split merge: kSlotCounters per slot, one per (sequence,
+// head group) of a launch. They start at zero when the library is loaded and every launch
+// returns the counters it uses to zero (the last arrival wraps them), so nothing clears them.
+// Consecutive launches take consecutive slots: launches on different streams only share
+// counters when kCounterSlots of them are in flight at once.
+constexpr int kSlotCounters = 8192;
+constexpr int kCounterSlots = 64;
+__device__ unsigned g_arrivals[kCounterSlots * kSlotCounters];
 
 struct SeqDesc {
     const uint8_t* k;     // layer cache base of this sequence
     const uint8_t* v;
     size_t part_off;      // floats: this sequence's partials (acc [hq][splits][128], then ml)
     int lk;               // keys
+    int chunk;            // keys per split (a function of lk alone)
     int splits;
     int split0;           // first grid column of this sequence
-    int pad;
 };
 
 template <int NS>
@@ -62,10 +91,10 @@ struct DecodeArgs {
     const float* q;       // [nseq, hq, 128]
     float* part;          // caller scratch
     void* o;              // [nseq, hq, 128]
+    unsigned* ctr;        // this launch's arrival counters [nseq][ngroups]
     int o_f16;
     int hq, hkv, group;   // group = hq / hkv
     int ngroups;          // head groups: hkv (one per KV head) or hq (one query head each)
-    int chunk;            // keys per split (the same for every sequence)
     int nseq;
     float scale;
     SeqDesc seq[NS];      // NS = 1 for single-sequence calls (smaller kernel arguments)
@@ -155,27 +184,221 @@ __device__ __forceinline__ int q8_exp(uint16_t sc) {
     return e == 0 ? -14 : min(e - 15, 9);
 }
 
+// ---- the end of a split: merge the W waves, then the splits --------------------------------
+// Device-coherent stores and loads (written through / read past the XCD's L2): a partial
+// stored by a workgroup on one XCD is then visible to the merging workgroup on any other.
+__device__ __forceinline__ void st_dev16(float* p, f32x4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void st_dev8(float* p, f32x2 v) {
+    asm volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ f32x4 ld_dev16(const float* p) {
+    f32x4 r;
+    asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(r) : "v"(p) : "memory");
+    return r;
+}
+__device__ __forceinline__ f32x2 ld_dev8(const float* p) {
+    f32x2 r;
+    asm volatile("global_load_dwordx2 %0, %1, off sc1" : "=v"(r) : "v"(p) : "memory");
+    return r;
+}
+
+// (M, A, L) <- merge of (M, A, L) and (m, a, l): M = max, weights 2^(m - M) (0 for an empty side)
+__device__ __forceinline__ void merge_split(float& M, f32x4& A, float& L, float m, f32x4 a,
+                                            float l) {
+    const float Mn = fmaxf(M, m);
+    const float w0 = (M == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(M - Mn);
+    const float w1 = (m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - Mn);
+    A = A * w0 + a * w1;
+    L = L * w0 + l * w1;
+    M = Mn;
+}
+
+template <int NS>
+__device__ __forceinline__ void store_out(const DecodeArgs<NS>& a, int si, int h, int d, f32x4 y) {
+    const size_t ob = ((size_t)si * a.hq + h) * kDim + d;
+    if (a.o_f16) {
+        u32x2 w;
+        w.x = pack2(f2h(y.x), f2h(y.y));
+        w.y = pack2(f2h(y.z), f2h(y.w));
+        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.o) + ob) = w;
+    } else {
+        *reinterpret_cast<f32x4*>(static_cast<float*>(a.o) + ob) = y;
+    }
+}
+
+// LDS floats finish_split needs: the W waves' states, then the final merge's split groups.
+template <int G, int W>
+constexpr int finish_floats() {
+    return W * G * (kDim + 2) > 64 * W * 6 ? W * G * (kDim + 2) : 64 * W * 6;
+}
+
+// Every thread of the workgroup calls this once its wave's blocks are done. The workgroup serves
+// HPW adjacent head groups (grid row `row`: head groups row * HPW ...), i.e. the HPW * G query
+// heads q0 = row * HPW * G ...; wave w works for head group w % HPW. Wave state: acc[dt] holds
+// O^T rows 16 dt + 4 u + r of column c16 (query head q0 + (w % HPW) G + c16 for c16 < G), already
+// summed over the hi / lo columns; mref the column's reference point (log2 domain, -inf for a
+// wave without keys) and lsum its softmax denominator (summed over the wave's rows). `lds` holds
+// finish_floats<G, W>() floats that no wave still reads.
+//  1. The W / HPW waves of each head group merge through LDS in wave order. A sequence with one
+//     split writes o here.
+//  2. Otherwise the workgroup stores its partials (acc [hq][splits][128], then (m, l)
+//     [hq][splits][2], the reference's scratch layout), waits until the stores are
+//     device-visible and increments the arrival counter of its (sequence, row) (atomic inc
+//     wrapping at splits - 1, so the last arrival leaves it at zero).
+//  3. The last arrival merges every split: thread (sg, cc, q) takes splits sg, sg + NSG, ... of
+//     query head q0 + cc, dims 4 q .. 4 q + 3, kPer per round trip; each round is folded as max
+//     first, then sum_r 2^(m_r - max) (acc_r, l_r) in split order (a short dependency chain),
+//     rounds and then the NSG split groups (through LDS) are folded the same way, and
+//     o = A / L is written. The order is fixed, so the result does not depend on which
+//     workgroup is last.
+template <int G, int W, int HPW, int NS>
+__device__ __forceinline__ void finish_split(const DecodeArgs<NS>& a, const SeqDesc& sd, int si,
+                                             int row, int split, float* lds,
+                                             const f32x4 (&acc)[8], float mref, float lsum) {
+    constexpr int KS = W / HPW;   // waves per head group
+    constexpr int HG = HPW * G;   // query heads of the workgroup
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int c16 = lane & 15;
+    const int u = lane >> 4;
+    float* m_acc = lds;                   // [W][G][128]
+    float* m_ml = lds + W * G * kDim;     // [W][G][2]
+    if (c16 < G) {
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+            *reinterpret_cast<f32x4*>(m_acc + (wave * G + c16) * kDim + 16 * dt + 4 * u) = acc[dt];
+        if (u == 0) *reinterpret_cast<f32x2*>(m_ml + (wave * G + c16) * 2) = f32x2{mref, lsum};
+    }
+    __syncthreads();
+    const int splits = sd.splits;
+    const int q0 = row * HG;
+    float* part_acc = a.part + sd.part_off;
+    float* part_ml = part_acc + (size_t)a.hq * splits * kDim;
+    for (int idx = threadIdx.x; idx < HG * 32; idx += 64 * W) {
+        const int hm = idx / (G * 32), c = (idx >> 5) % G, d = 4 * (idx & 31);
+        const int h = q0 + hm * G + c;
+        if (h >= a.hq) continue;  // a partial last row of head groups
+        float M = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) M = fmaxf(M, m_ml[((k * HPW + hm) * G + c) * 2]);
+        f32x4 A = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        float L = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            const int wv = (k * HPW + hm) * G + c;
+            const float mw = m_ml[wv * 2];
+            const float e = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+            A += e * *reinterpret_cast<const f32x4*>(m_acc + wv * kDim + d);
+            L += e * m_ml[wv * 2 + 1];
+        }
+        if (splits == 1) {
+            store_out(a, si, h, d, A / L);
+        } else {
+            st_dev16(part_acc + ((size_t)h * splits + split) * kDim + d, A);
+            if (d == 0) st_dev8(part_ml + ((size_t)h * splits + split) * 2, f32x2{M, L});
+        }
+    }
+    if (splits == 1) return;
+    __shared__ int s_last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores are visible
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int rows = (a.ngroups + HPW - 1) / HPW;
+        unsigned* ctr = a.ctr + si * rows + row;
+        const unsigned t = __builtin_amdgcn_atomic_inc32(ctr, (unsigned)(splits - 1),
+                                                         __ATOMIC_RELAXED, "agent");
+        s_last = t == (unsigned)(splits - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+
+    constexpr int NSG = 64 * W / (HG * 32);  // split groups
+    static_assert(NSG >= 1 && NSG * HG * 32 == 64 * W, "final-merge thread layout");
+    const int q = threadIdx.x & 31, cc = (threadIdx.x >> 5) % HG, sg = threadIdx.x / (32 * HG);
+    const int h = min(q0 + cc, a.hq - 1);  // (duplicate work past hq is not stored)
+    const float* pa = part_acc + (size_t)h * splits * kDim + 4 * q;
+    const float* pm = part_ml + (size_t)h * splits * 2;
+    float M = -INFINITY, L = 0.0f;
+    f32x4 A = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    constexpr int kPer = 8;  // splits per thread per round trip
+    for (int s0 = sg; s0 < splits; s0 += kPer * NSG) {
+        f32x4 av[kPer];
+        f32x2 mv[kPer];
+#pragma unroll
+        for (int r = 0; r < kPer; ++r) {
+            const int sp = min(s0 + NSG * r, splits - 1);
+            av[r] = ld_dev16(pa + (size_t)sp * kDim);
+            mv[r] = ld_dev8(pm + (size_t)sp * 2);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int r = 0; r < kPer; ++r) asm volatile("" : "+v"(av[r]), "+v"(mv[r]));
+        // this round's splits: max first, then the weighted sums in split order
+        float Mr = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < kPer; ++r)
+            if (s0 + NSG * r < splits) Mr = fmaxf(Mr, mv[r].x);
+        f32x4 Ar = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        float Lr = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kPer; ++r) {
+            const bool ok = s0 + NSG * r < splits && mv[r].x != -INFINITY;
+            const float w = ok ? __builtin_amdgcn_exp2f(mv[r].x - Mr) : 0.0f;
+            Ar += w * av[r];
+            Lr += w * mv[r].y;
+        }
+        merge_split(M, A, L, Mr, Ar, Lr);
+    }
+    if constexpr (NSG > 1) {
+        f32x4* r_a = reinterpret_cast<f32x4*>(lds);  // [NSG][HG][32], then m and l
+        float* r_m = lds + 4 * 64 * W;
+        float* r_l = r_m + 64 * W;
+        r_a[threadIdx.x] = A;
+        r_m[threadIdx.x] = M;
+        r_l[threadIdx.x] = L;
+        __syncthreads();
+        if (sg != 0) return;
+        float Mx = M;
+#pragma unroll
+        for (int k = 1; k < NSG; ++k) Mx = fmaxf(Mx, r_m[threadIdx.x + k * HG * 32]);
+        A = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        L = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NSG; ++k) {
+            const int t = threadIdx.x + k * HG * 32;
+            const float mk = r_m[t];
+            const float w = mk == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mk - Mx);
+            A += w * r_a[t];
+            L += w * r_l[t];
+        }
+    }
+    if (q0 + cc < a.hq) store_out(a, si, q0 + cc, 4 * q, A / L);
+}
+
 // ---- f32 caches (the reference's exact variant): register-staged K and V -------------------
-// One wave per head group and split. K and V rows are loaded into registers (the next block's
-// loads in flight while the current block is computed) and split into f16 hi + lo halves; V goes
-// through a wave-private padded LDS tile (hi and lo) to be read transposed.
-template <int G, int NS>
-__global__ void __launch_bounds__(64 * kMaxWaves)
+// Workgroup = one head group x one split, W waves walking the split's blocks w, w + W, ... K and
+// V rows are loaded into registers (the next block's loads in flight while the current block is
+// computed) and split into f16 hi + lo halves; V goes through a wave-private padded LDS tile (hi
+// and lo) to be read transposed.
+template <int G, int NS, int W>
+__global__ void __launch_bounds__(64 * W)
 decode_f32_kernel(DecodeArgs<NS> a) {
     constexpr int RB = KvTraits<BRASA_KV_F32>::row_bytes;
-    constexpr int kWaves = kMaxWaves;
     constexpr int kVTile = 2 * kBlock * kVStr;
 
-    __shared__ __attribute__((aligned(16))) uint16_t s_v[kWaves][kVTile];
+    __shared__ __attribute__((aligned(16))) uint16_t s_v[W][kVTile];
+    __shared__ __attribute__((aligned(16))) float s_fin[finish_floats<G, W>()];
 
-    const int si = seq_of(a, blockIdx.x);
+    const int hg = blockIdx.x % a.ngroups;  // this workgroup's head group
+    const int col = blockIdx.x / a.ngroups;
+    const int si = seq_of(a, col);
     const SeqDesc& sd = a.seq[si];
-    const int split = blockIdx.x - sd.split0;
+    const int split = col - sd.split0;
     const float* qseq = a.q + (size_t)si * a.hq * kDim;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int hg = blockIdx.y * (int)(blockDim.x >> 6) + wave;  // this wave's head group
-    if (hg >= a.ngroups) return;           // (no workgroup barrier follows)
     const int h0 = hg * G;                 // its first query head
     const int kh = h0 / a.group;           // its KV head
     const int c16 = lane & 15;             // MFMA row/column index
@@ -203,8 +426,10 @@ decode_f32_kernel(DecodeArgs<NS> a) {
         qb[t] = col_lo ? lo : hi;
     }
 
-    const int s0 = split * a.chunk;
-    const int s1 = min(sd.lk, s0 + a.chunk);
+    const int s0 = split * sd.chunk;
+    const int s1 = min(sd.lk, s0 + sd.chunk);
+    const int nblk = (s1 - s0 + kBlock - 1) / kBlock;
+    const int nb = nblk > wave ? (nblk - wave + W - 1) / W : 0;  // this wave's blocks
     const size_t kstride = (size_t)a.hkv * RB;
     const uint8_t* kbase = sd.k + (size_t)kh * RB;
     const uint8_t* vbase = sd.v + (size_t)kh * RB;
@@ -304,22 +529,21 @@ decode_f32_kernel(DecodeArgs<NS> a) {
         }
     };
 
-    // ---- stream the split's 32-key blocks, the next block's loads in flight -----------------
-    int jb = s0;
-    {
+    // ---- stream this wave's 32-key blocks, the next block's loads in flight -----------------
+    if (nb > 0) {
+        auto blk = [&](int i) { return s0 + kBlock * (wave + W * i); };
         F32Block A, B;
-        load(A, jb);
+        load(A, blk(0));
         // the prefetch is unconditional (rows clamp to s1 - 1): a branch around it would make
         // the compiler wait for every outstanding load before the current block's V writes
+        int i = 0;
         while (true) {
-            load(B, jb + kBlock);
-            compute(A, jb);
-            jb += kBlock;
-            if (jb >= s1) break;
-            load(A, jb + kBlock);
-            compute(B, jb);
-            jb += kBlock;
-            if (jb >= s1) break;
+            load(B, blk(i + 1));
+            compute(A, blk(i));
+            if (++i >= nb) break;
+            load(A, blk(i + 1));
+            compute(B, blk(i));
+            if (++i >= nb) break;
         }
     }
 
@@ -331,56 +555,24 @@ decode_f32_kernel(DecodeArgs<NS> a) {
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[dt][i] += __shfl_xor(acc[dt][i], G, 64);
-    if (!colq) return;
-    const int hh = h0 + c16;
-    const int splits = sd.splits;
-    if (splits == 1) {
-        const float inv = 1.0f / lsum;
-        const size_t ob = ((size_t)si * a.hq + hh) * kDim;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-            const int d = 16 * dt + 4 * u;
-            const f32x4 y = acc[dt] * inv;
-            if (a.o_f16) {
-                u32x2 w;
-                w.x = pack2(f2h(y.x), f2h(y.y));
-                w.y = pack2(f2h(y.z), f2h(y.w));
-                *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.o) + ob + d) = w;
-            } else {
-                *reinterpret_cast<f32x4*>(static_cast<float*>(a.o) + ob + d) = y;
-            }
-        }
-        return;
-    }
-    float* acc_out = a.part + sd.part_off + ((size_t)hh * splits + split) * kDim;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-        *reinterpret_cast<f32x4*>(acc_out + 16 * dt + 4 * u) = acc[dt];
-    if (u == 0) {
-        float* ml_out = a.part + sd.part_off + (size_t)a.hq * splits * kDim;
-        *reinterpret_cast<f32x2*>(ml_out + ((size_t)hh * splits + split) * 2) = f32x2{m2[0], lsum};
-    }
+    finish_split<G, W, 1>(a, sd, si, hg, split, s_fin, acc, m2[0], lsum);
 }
 
-// ---- f16 caches: HPW head groups x KS key slices per workgroup, every load explicit -----------
-// Workgroup = HPW * KS wave64: HPW adjacent head groups (a KV head and its G query heads) x one
-// split of `chunk` keys. Wave (hl, ks) = (wave % HPW, wave / HPW) walks the 32-key blocks ks,
-// ks + KS, ks + 2 KS, ... of the split for head group hl, so at any time the workgroup reads HPW
-// adjacent KV heads' rows (HPW * 256 contiguous bytes per key: a workgroup that reads one head's
-// 256-byte rows at the 2 KB stride of the cache loads the HBM channels unevenly and was measured
-// ~20 % slower at 16K keys). A wave keeps up to kRing blocks in flight: K rows go from HBM into
-// registers (the MFMA A operand), V rows HBM -> LDS (global_load_lds_dwordx4, read transposed by
-// ds_read_tr16_b64), Q into registers. Every vector-memory instruction of the kernel is inline
-// asm, issued in a fixed order, so each wait is an exact count: block i is ready when the blocks
-// issued after it (at most kRing - 1, 16 instructions each) are the only ones pending. The wait
-// names the registers it guards as operands, so no use of them can be scheduled above it.
-// Block i + kRing is issued into block i's ring slot once block i has been computed.
+// ---- f16 caches: every load explicit --------------------------------------------------------
+// Workgroup = HPW adjacent head groups x one split of sd.chunk keys, W wave64; wave w works for
+// head group w % HPW and walks the 32-key blocks ks, ks + KS, ... of the split (ks = w / HPW,
+// KS = W / HPW), so at any time the workgroup reads HPW adjacent KV heads' rows. A wave keeps up to kRing blocks in flight: K rows go
+// from HBM into registers (the MFMA A operand), V rows HBM -> LDS (global_load_lds_dwordx4, read
+// transposed by ds_read_tr16_b64), Q into registers. Every vector-memory instruction of the
+// block loop is inline asm, issued in a fixed order, so each wait is an exact count: block i is
+// ready when the blocks issued after it (at most kRing - 1, 16 instructions each) are the only
+// ones pending. The wait names the registers it guards as operands, so no use of them can be
+// scheduled above it. Block i + kRing is issued into block i's ring slot once block i has been
+// computed.
 // Softmax: columns c < G hold the hi halves of the split Q / P operands, G <= c < 2 G the lo
 // halves; one DPP exchange adds them (the same bits in both lanes). The running max is lazy: the
 // reference point moves only when a block's max exceeds it by more than 2^8, so most blocks skip
-// the rescale of O. After the split the KS waves of each head group merge (m, l, acc) through LDS
-// and the workgroup writes one partial per query head (or the output when the sequence has one
-// split).
+// the rescale of O.
 constexpr int kRing = 2;                    // blocks in flight per wave (16 instructions each)
 constexpr int kMaxLdsWaves = 8;
 constexpr int kTileHalves = kBlock * kDim;  // one 32 x 128 f16 tile = 8 KB
@@ -430,21 +622,21 @@ __device__ __forceinline__ float sum_rows(float x) {
     return __int_as_float(b[0]) + __int_as_float(b[1]);
 }
 
-template <int G, int NS, int HPW, int KS>
-__global__ void __launch_bounds__(64 * HPW * KS)
+template <int G, int NS, int HPW, int W>
+__global__ void __launch_bounds__(64 * W)
 decode_f16_kernel(DecodeArgs<NS> a) {
     constexpr int RB = 256;
-    constexpr int W = HPW * KS;
+    constexpr int KS = W / HPW;
     static_assert(W <= kMaxLdsWaves, "waves per workgroup");
     __shared__ __attribute__((aligned(16))) uint16_t s_v[W][kRing][kTileHalves];
-    constexpr int kMergeFloats = W * G * (kDim + 2);
-    constexpr bool kSepMerge = W * kRing * kTileHalves * 2 + kMergeFloats * 4 <= 160 * 1024;
-    __shared__ __attribute__((aligned(16))) float s_m[kSepMerge ? kMergeFloats : 1];
+    constexpr int kFin = finish_floats<G, W>();
+    constexpr bool kSepFin = W * kRing * kTileHalves * 2 + kFin * 4 <= 160 * 1024;
+    __shared__ __attribute__((aligned(16))) float s_fin[kSepFin ? kFin : 1];
 
-    // 1-D grid, head-group rows innermost: consecutive workgroups read the same keys of
-    // adjacent KV heads
+    // grid: (split column, row of HPW head groups), rows innermost
     const int rows = (a.ngroups + HPW - 1) / HPW;
-    const int col = blockIdx.x / rows, row = blockIdx.x - col * rows;
+    const int row = blockIdx.x % rows;
+    const int col = blockIdx.x / rows;
     const int si = seq_of(a, col);
     const SeqDesc& sd = a.seq[si];
     const int split = col - sd.split0;
@@ -452,17 +644,17 @@ decode_f16_kernel(DecodeArgs<NS> a) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int hl = wave % HPW, ks = wave / HPW;
-    const int hg = row * HPW + hl;  // this wave's head group
+    const int hg = row * HPW + hl;                 // this wave's head group
     const bool hg_ok = hg < a.ngroups;
-    const int h0 = min(hg, a.ngroups - 1) * G;  // its first query head
-    const int kh = h0 / a.group;                 // its KV head
+    const int h0 = min(hg, a.ngroups - 1) * G;     // its first query head
+    const int kh = h0 / a.group;                   // its KV head
     const int c16 = lane & 15;
     const int u = lane >> 4;
     const bool colq = c16 < G;
     const bool col_lo = c16 >= G && c16 < 2 * G;
 
-    const int s0 = split * a.chunk;
-    const int s1 = min(sd.lk, s0 + a.chunk);
+    const int s0 = split * sd.chunk;
+    const int s1 = min(sd.lk, s0 + sd.chunk);
     const int nblk = (s1 - s0 + kBlock - 1) / kBlock;
     // this wave's blocks: ks, ks + KS, ...
     const int nb = (hg_ok && nblk > ks) ? (nblk - ks + KS - 1) / KS : 0;
@@ -605,70 +797,22 @@ decode_f16_kernel(DecodeArgs<NS> a) {
         step(I1{}, i0 + 1);
     }
 
-    // ---- merge the KS waves of each head group through LDS -------------------------------------
+    // ---- the split's end ---------------------------------------------------------------------
     lsum = sum_rows(lsum);
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[dt][r] += xor_row<G>(acc[dt][r], c16);
-    // The merge area has its own LDS when it fits beside the ring (one barrier); otherwise it
-    // reuses the V slots once every wave is done with them (all copies waited for).
-    float* m_acc;
-    if constexpr (kSepMerge) {
-        m_acc = s_m;
+    // the merge area has its own LDS when it fits beside the ring; otherwise it reuses the V
+    // slots once every wave is done with them (all copies waited for)
+    float* fin;
+    if constexpr (kSepFin) {
+        fin = s_fin;
     } else {
         __syncthreads();
-        m_acc = reinterpret_cast<float*>(&s_v[0][0][0]);
+        fin = reinterpret_cast<float*>(&s_v[0][0][0]);
     }
-    float* m_ml = m_acc + W * G * kDim;  // m_acc: [wave][G][128], m_ml: [wave][G][2]
-    if (colq) {
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-            *reinterpret_cast<f32x4*>(m_acc + (wave * G + c16) * kDim + 16 * dt + 4 * u) = acc[dt];
-        // a wave without blocks reports m = -inf and l = 0
-        if (u == 0) *reinterpret_cast<f32x2*>(m_ml + (wave * G + c16) * 2) = f32x2{mref, lsum};
-    }
-    __syncthreads();
-    const int splits = sd.splits;
-    for (int idx = threadIdx.x; idx < HPW * G * (kDim / 4); idx += 64 * W) {
-        const int d = 4 * (idx % (kDim / 4));
-        const int c = (idx / (kDim / 4)) % G;
-        const int hm = idx / (G * (kDim / 4));  // head group within the workgroup
-        if (row * HPW + hm >= a.ngroups) continue;
-        float M = -INFINITY;
-#pragma unroll
-        for (int k = 0; k < KS; ++k) M = fmaxf(M, m_ml[((k * HPW + hm) * G + c) * 2]);
-        f32x4 A = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        float L = 0.0f;
-#pragma unroll
-        for (int k = 0; k < KS; ++k) {
-            const int wv = k * HPW + hm;
-            const float mw = m_ml[(wv * G + c) * 2];
-            const float e = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-            A += e * *reinterpret_cast<const f32x4*>(m_acc + (wv * G + c) * kDim + d);
-            L += e * m_ml[(wv * G + c) * 2 + 1];
-        }
-        const int hh = (row * HPW + hm) * G + c;
-        if (splits == 1) {
-            const float inv = 1.0f / L;
-            const f32x4 y = A * inv;
-            const size_t ob = ((size_t)si * a.hq + hh) * kDim + d;
-            if (a.o_f16) {
-                u32x2 w;
-                w.x = pack2(f2h(y.x), f2h(y.y));
-                w.y = pack2(f2h(y.z), f2h(y.w));
-                *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.o) + ob) = w;
-            } else {
-                *reinterpret_cast<f32x4*>(static_cast<float*>(a.o) + ob) = y;
-            }
-        } else {
-            *reinterpret_cast<f32x4*>(a.part + sd.part_off + ((size_t)hh * splits + split) * kDim + d) = A;
-            if (d == 0) {
-                float* ml_out = a.part + sd.part_off + (size_t)a.hq * splits * kDim;
-                *reinterpret_cast<f32x2*>(ml_out + ((size_t)hh * splits + split) * 2) = f32x2{M, L};
-            }
-        }
-    }
+    finish_split<G, W, HPW>(a, sd, si, row, split, fin, acc, mref, lsum);
 }
 
 // ---- q8_0 caches: the f16 kernel's structure with codes and scales staged in LDS -----------
@@ -714,16 +858,18 @@ __device__ __forceinline__ void codes4_to_f16(uint32_t w, uint32_t& lo, uint32_t
     hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, h) + bias);
 }
 
-template <int G, int NS, int HPW, int KS>
-__global__ void __launch_bounds__(64 * HPW * KS)
+template <int G, int NS, int HPW, int W>
+__global__ void __launch_bounds__(64 * W)
 decode_q8_kernel(DecodeArgs<NS> a) {
     constexpr int RB = kQ8Row;
-    constexpr int W = HPW * KS;
+    constexpr int KS = W / HPW;
     static_assert(W <= kMaxLdsWaves, "waves per workgroup");
+    static_assert(finish_floats<G, W>() * 4 <= W * kRing * kQ8Slot, "merge area in the ring");
     __shared__ __attribute__((aligned(16))) uint8_t s_slot[W][kRing][kQ8Slot];
 
     const int rows = (a.ngroups + HPW - 1) / HPW;
-    const int col = blockIdx.x / rows, row = blockIdx.x - col * rows;
+    const int row = blockIdx.x % rows;
+    const int col = blockIdx.x / rows;
     const int si = seq_of(a, col);
     const SeqDesc& sd = a.seq[si];
     const int split = col - sd.split0;
@@ -740,8 +886,8 @@ decode_q8_kernel(DecodeArgs<NS> a) {
     const bool colq = c16 < G;
     const bool col_lo = c16 >= G && c16 < 2 * G;
 
-    const int s0 = split * a.chunk;
-    const int s1 = min(sd.lk, s0 + a.chunk);
+    const int s0 = split * sd.chunk;
+    const int s1 = min(sd.lk, s0 + sd.chunk);
     const int nblk = (s1 - s0 + kBlock - 1) / kBlock;
     const int nb = (hg_ok && nblk > ks) ? (nblk - ks + KS - 1) / KS : 0;
     const size_t kstride = (size_t)a.hkv * RB;
@@ -961,237 +1107,71 @@ decode_q8_kernel(DecodeArgs<NS> a) {
         step(I1{}, i0 + 1);
     }
 
-    // ---- merge the KS waves of each head group through LDS -------------------------------------
+    // ---- the split's end ---------------------------------------------------------------------
     lsum = sum_rows(lsum);
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[dt][r] += xor_row<G>(acc[dt][r], c16);
-    __syncthreads();  // every wave is done with its V slots (all copies waited for)
-    float* m_acc = reinterpret_cast<float*>(&s_slot[0][0][0]);         // [wave][G][128]
-    float* m_ml = m_acc + W * G * kDim;                                // [wave][G][2]
-    if (colq) {
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-            *reinterpret_cast<f32x4*>(m_acc + (wave * G + c16) * kDim + 16 * dt + 4 * u) = acc[dt];
-        // a wave without blocks reports m = -inf and l = 0
-        if (u == 0) *reinterpret_cast<f32x2*>(m_ml + (wave * G + c16) * 2) = f32x2{mref, lsum};
-    }
-    __syncthreads();
-    const int splits = sd.splits;
-    for (int idx = threadIdx.x; idx < HPW * G * (kDim / 4); idx += 64 * W) {
-        const int d = 4 * (idx % (kDim / 4));
-        const int c = (idx / (kDim / 4)) % G;
-        const int hm = idx / (G * (kDim / 4));  // head group within the workgroup
-        if (row * HPW + hm >= a.ngroups) continue;
-        float M = -INFINITY;
-#pragma unroll
-        for (int k = 0; k < KS; ++k) M = fmaxf(M, m_ml[((k * HPW + hm) * G + c) * 2]);
-        f32x4 A = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        float L = 0.0f;
-#pragma unroll
-        for (int k = 0; k < KS; ++k) {
-            const int wv = k * HPW + hm;
-            const float mw = m_ml[(wv * G + c) * 2];
-            const float e = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-            A += e * *reinterpret_cast<const f32x4*>(m_acc + (wv * G + c) * kDim + d);
-            L += e * m_ml[(wv * G + c) * 2 + 1];
-        }
-        const int hh = (row * HPW + hm) * G + c;
-        if (splits == 1) {
-            const float inv = 1.0f / L;
-            const f32x4 y = A * inv;
-            const size_t ob = ((size_t)si * a.hq + hh) * kDim + d;
-            if (a.o_f16) {
-                u32x2 w;
-                w.x = pack2(f2h(y.x), f2h(y.y));
-                w.y = pack2(f2h(y.z), f2h(y.w));
-                *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.o) + ob) = w;
-            } else {
-                *reinterpret_cast<f32x4*>(static_cast<float*>(a.o) + ob) = y;
-            }
-        } else {
-            *reinterpret_cast<f32x4*>(a.part + sd.part_off + ((size_t)hh * splits + split) * kDim + d) = A;
-            if (d == 0) {
-                float* ml_out = a.part + sd.part_off + (size_t)a.hq * splits * kDim;
-                *reinterpret_cast<f32x2*>(ml_out + ((size_t)hh * splits + split) * 2) = f32x2{M, L};
-            }
-        }
-    }
+    __syncthreads();  // every wave is done with its slots (all copies waited for)
+    finish_split<G, W, HPW>(a, sd, si, row, split, reinterpret_cast<float*>(&s_slot[0][0][0]),
+                            acc, mref, lsum);
 }
 
-// Second pass (attn_decode_reduce, decode_attention.metal:68-84): one workgroup of 4 waves per
-// (query head, 32-dim quarter, sequence). Thread t owns dims 4 (t % 8) .. + 4 of the quarter and
-// the splits t / 8 + 32 j; it loads kRedPer of them per round trip and folds them with the
-// running-max form of the split merge, o = sum_s w_s acc_s / sum_s w_s l_s with
-// w_s = 2^(m_s - max m). The 8 split lanes of a wave are merged by a butterfly over lane bits 3, 4
-// and 5 (DPP and permlane swaps: both partners compute the same merge, so the bits agree) and the
-// 4 waves through LDS in a fixed order, so the result is reproducible bit for bit.
-constexpr int kRedThreads = 256;
-constexpr int kRedDims = 32;                               // dims per workgroup
-constexpr int kRedLanes = kRedThreads / (kRedDims / 4);   // 32 split lanes
-constexpr int kRedPer = 4;                                 // splits per lane per round trip
 
-struct ReduceArgs {
-    const float* part;
-    void* o;
-    int o_f16, hq, nseq;
-    int splits[kMaxSeqs];
-    size_t part_off[kMaxSeqs];
-};
+template <int KV> struct KernelFor;
+template <> struct KernelFor<BRASA_KV_F16> { static constexpr int W = kWavesF16; };
+template <> struct KernelFor<BRASA_KV_Q8_0> { static constexpr int W = kWavesQ8; };
+template <> struct KernelFor<BRASA_KV_F32> { static constexpr int W = kWavesF32; };
 
-// (M, A, L) <- merge of (M, A, L) and (m, a, l): M = max, weights 2^(m - M) (0 for an empty side)
-__device__ __forceinline__ void merge_split(float& M, f32x4& A, float& L, float m, f32x4 a,
-                                            float l) {
-    const float Mn = fmaxf(M, m);
-    const float w0 = (M == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(M - Mn);
-    const float w1 = (m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - Mn);
-    A = A * w0 + a * w1;
-    L = L * w0 + l * w1;
-    M = Mn;
-}
-
-// value of lane l ^ 8 (DPP row_ror:8), l ^ 16 (permlane16_swap), l ^ 32 (permlane32_swap)
-template <int M>
-__device__ __forceinline__ float lane_xor(float x, int lane) {
-    if constexpr (M == 8) {
-        return dpp<0x128>(x);
-    } else if constexpr (M == 16) {
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
-        return __int_as_float((lane & 16) ? r[0] : r[1]);
-    } else {
-        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
-        return __int_as_float((lane & 32) ? r[0] : r[1]);
-    }
-}
-template <int M>
-__device__ __forceinline__ void merge_lanes(float& Mx, f32x4& A, float& L, int lane) {
-    const float m1 = lane_xor<M>(Mx, lane), l1 = lane_xor<M>(L, lane);
-    const f32x4 a1 = f32x4{lane_xor<M>(A.x, lane), lane_xor<M>(A.y, lane), lane_xor<M>(A.z, lane),
-                           lane_xor<M>(A.w, lane)};
-    merge_split(Mx, A, L, m1, a1, l1);
-}
-
-__global__ void __launch_bounds__(kRedThreads) decode_reduce_kernel(ReduceArgs ra) {
-    const int si = blockIdx.z;
-    const int splits = ra.splits[si];
-    if (splits == 1) return;  // the split kernel wrote this sequence's output
-    const float* part = ra.part + ra.part_off[si];
-    const int hq = ra.hq;
-    const int h = blockIdx.x, d0 = kRedDims * blockIdx.y;
-    const int t = threadIdx.x, q4 = t & 7, sl = t >> 3;
-    const int lane = t & 63, wave = t >> 6;
-    const f32x4* acc = reinterpret_cast<const f32x4*>(part + (size_t)h * splits * kDim + d0) + q4;
-    const f32x2* ml = reinterpret_cast<const f32x2*>(part + (size_t)hq * splits * kDim) + (size_t)h * splits;
-    float M = -INFINITY, L = 0.0f;
-    f32x4 A = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int s0 = sl; s0 < splits; s0 += kRedLanes * kRedPer) {
-        f32x2 mlv[kRedPer];
-        f32x4 av[kRedPer];
-#pragma unroll
-        for (int r = 0; r < kRedPer; ++r) {
-            const int sp = min(s0 + kRedLanes * r, splits - 1);
-            mlv[r] = ml[sp];
-            av[r] = acc[(size_t)sp * (kDim / 4)];
-        }
-#pragma unroll
-        for (int r = 0; r < kRedPer; ++r)
-            if (s0 + kRedLanes * r < splits) merge_split(M, A, L, mlv[r].x, av[r], mlv[r].y);
-    }
-    merge_lanes<8>(M, A, L, lane);
-    merge_lanes<16>(M, A, L, lane);
-    merge_lanes<32>(M, A, L, lane);
-    __shared__ f32x4 s_a[4][8];
-    __shared__ float s_m[4][8], s_l[4][8];
-    if (lane < 8) {
-        s_a[wave][lane] = A;
-        s_m[wave][lane] = M;
-        s_l[wave][lane] = L;
-    }
-    __syncthreads();
-    if (t >= 8) return;
-    M = s_m[0][t];
-    A = s_a[0][t];
-    L = s_l[0][t];
-#pragma unroll
-    for (int w = 1; w < 4; ++w) merge_split(M, A, L, s_m[w][t], s_a[w][t], s_l[w][t]);
-    const f32x4 y = A / L;
-    const size_t off = ((size_t)si * hq + h) * kDim + d0 + 4 * t;
-    if (ra.o_f16) {
-        u32x2 w;
-        w.x = pack2(f2h(y.x), f2h(y.y));
-        w.y = pack2(f2h(y.z), f2h(y.w));
-        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(ra.o) + off) = w;
-    } else {
-        *reinterpret_cast<f32x4*>(static_cast<float*>(ra.o) + off) = y;
-    }
-}
-
-// Launch shape chosen by decode_plan: keys per split, and the workgroup layout (head groups x
-// key slices for f16 caches, head groups of one wave each for the other caches).
-struct Plan {
-    int chunk;
-    int waves;  // register-staged kernel: head groups per workgroup
-    int hpw;    // f16 kernel: head groups per workgroup
-    int ks;     // f16 kernel: key slices (waves) per head group
-};
-
-template <int G, int NS, int HPW, int KS>
-int launch_f16(const DecodeArgs<NS>& a, int cols, hipStream_t stream) {
+template <int KV, int G, int NS, int HPW>
+int launch_hpw(const DecodeArgs<NS>& a, int cols, hipStream_t stream) {
+    constexpr int W = KernelFor<KV>::W;
     const int rows = (a.ngroups + HPW - 1) / HPW;
-    hipLaunchKernelGGL((decode_f16_kernel<G, NS, HPW, KS>), dim3(cols * rows), dim3(64 * HPW * KS),
-                       0, stream, a);
-    return check_launch("decode_f16_kernel");
-}
-
-template <int G, int NS, int HPW, int KS>
-int launch_q8(const DecodeArgs<NS>& a, int cols, hipStream_t stream) {
-    const int rows = (a.ngroups + HPW - 1) / HPW;
-    hipLaunchKernelGGL((decode_q8_kernel<G, NS, HPW, KS>), dim3(cols * rows), dim3(64 * HPW * KS),
-                       0, stream, a);
-    return check_launch("decode_q8_kernel");
+    const dim3 grid(cols * rows), block(64 * W);
+    if constexpr (KV == BRASA_KV_F16) {
+        hipLaunchKernelGGL((decode_f16_kernel<G, NS, HPW, W>), grid, block, 0, stream, a);
+        return check_launch("decode_f16_kernel");
+    } else {
+        hipLaunchKernelGGL((decode_q8_kernel<G, NS, HPW, W>), grid, block, 0, stream, a);
+        return check_launch("decode_q8_kernel");
+    }
 }
 
 template <int KV, int G, int NS>
-int launch(const DecodeArgs<NS>& a, const Plan& p, hipStream_t stream) {
-    const int cols = a.seq[a.nseq - 1].split0 + a.seq[a.nseq - 1].splits;
-    if constexpr (KV == BRASA_KV_F16) {
-        if (p.hpw == 4 && p.ks == 2) return launch_f16<G, NS, 4, 2>(a, cols, stream);
-        if (p.hpw == 2 && p.ks == 4) return launch_f16<G, NS, 2, 4>(a, cols, stream);
-        if (p.hpw == 1 && p.ks == 8) return launch_f16<G, NS, 1, 8>(a, cols, stream);
-        if (p.hpw == 1 && p.ks == 4) return launch_f16<G, NS, 1, 4>(a, cols, stream);
-        return set_error(BRASA_ERR_UNSUPPORTED, "decode: layout %d x %d not compiled", p.hpw, p.ks);
-    } else if constexpr (KV == BRASA_KV_Q8_0) {
-        if (p.hpw == 4 && p.ks == 2) return launch_q8<G, NS, 4, 2>(a, cols, stream);
-        if (p.hpw == 2 && p.ks == 4) return launch_q8<G, NS, 2, 4>(a, cols, stream);
-        if (p.hpw == 1 && p.ks == 8) return launch_q8<G, NS, 1, 8>(a, cols, stream);
-        if (p.hpw == 1 && p.ks == 4) return launch_q8<G, NS, 1, 4>(a, cols, stream);
-        return set_error(BRASA_ERR_UNSUPPORTED, "decode: layout %d x %d not compiled", p.hpw, p.ks);
-    } else {
-        const int rows = (a.ngroups + p.waves - 1) / p.waves;
-        hipLaunchKernelGGL((decode_f32_kernel<G, NS>), dim3(cols, rows), dim3(64 * p.waves), 0,
+int launch(const DecodeArgs<NS>& a, int hpw, int cols, hipStream_t stream) {
+    if constexpr (KV == BRASA_KV_F32) {
+        constexpr int W = KernelFor<KV>::W;
+        hipLaunchKernelGGL((decode_f32_kernel<G, NS, W>), dim3(cols * a.ngroups), dim3(64 * W), 0,
                            stream, a);
         return check_launch("decode_f32_kernel");
+    } else {
+        if (hpw == 1) return launch_hpw<KV, G, NS, 1>(a, cols, stream);
+        if constexpr (2 * G <= kMaxMergeHeads)
+            if (hpw == 2) return launch_hpw<KV, G, NS, 2>(a, cols, stream);
+        if constexpr (4 * G <= kMaxMergeHeads)
+            if (hpw == 4) return launch_hpw<KV, G, NS, 4>(a, cols, stream);
+        return set_error(BRASA_ERR_UNSUPPORTED, "decode: %d head groups per workgroup not compiled", hpw);
     }
 }
 
 template <int KV, int NS>
-int launch_g(const DecodeArgs<NS>& a, int G, const Plan& p, hipStream_t stream) {
+int launch_g(const DecodeArgs<NS>& a, int G, int hpw, int cols, hipStream_t stream) {
     switch (G) {
-        case 1: return launch<KV, 1, NS>(a, p, stream);
-        case 2: return launch<KV, 2, NS>(a, p, stream);
-        case 4: return launch<KV, 4, NS>(a, p, stream);
-        case 8: return launch<KV, 8, NS>(a, p, stream);
+        case 1: return launch<KV, 1, NS>(a, hpw, cols, stream);
+        case 2: return launch<KV, 2, NS>(a, hpw, cols, stream);
+        case 4: return launch<KV, 4, NS>(a, hpw, cols, stream);
+        case 8: return launch<KV, 8, NS>(a, hpw, cols, stream);
     }
     return set_error(BRASA_ERR_UNSUPPORTED, "decode: GQA group %d not compiled", G);
 }
 
 template <int NS>
-int launch_kv(const DecodeArgs<NS>& a, int kv, int G, const Plan& p, hipStream_t stream) {
+int launch_kv(const DecodeArgs<NS>& a, int kv, int G, int hpw, int cols, hipStream_t stream) {
     switch (kv) {
-        case BRASA_KV_F32: return launch_g<BRASA_KV_F32>(a, G, p, stream);
-        case BRASA_KV_F16: return launch_g<BRASA_KV_F16>(a, G, p, stream);
-        case BRASA_KV_Q8_0: return launch_g<BRASA_KV_Q8_0>(a, G, p, stream);
+        case BRASA_KV_F32: return launch_g<BRASA_KV_F32>(a, G, hpw, cols, stream);
+        case BRASA_KV_F16: return launch_g<BRASA_KV_F16>(a, G, hpw, cols, stream);
+        case BRASA_KV_Q8_0: return launch_g<BRASA_KV_Q8_0>(a, G, hpw, cols, stream);
     }
     return set_error(BRASA_ERR_ARG, "decode: invalid kv type %d", kv);
 }
@@ -1202,62 +1182,76 @@ DecodeArgs<1> one_seq(const DecodeArgs<kMaxSeqs>& a) {
     b.q = a.q;
     b.part = a.part;
     b.o = a.o;
+    b.ctr = a.ctr;
     b.o_f16 = a.o_f16;
     b.hq = a.hq;
     b.hkv = a.hkv;
     b.group = a.group;
     b.ngroups = a.ngroups;
-    b.chunk = a.chunk;
     b.nseq = 1;
     b.scale = a.scale;
     b.seq[0] = a.seq[0];
     return b;
 }
 
+// Device address of the arrival counters, looked up once per device.
+constexpr int kMaxDevices = 64;
+unsigned* g_ctr_base[kMaxDevices];
+std::once_flag g_ctr_once[kMaxDevices];
+std::atomic<unsigned> g_next_slot{0};
+
+int arrival_counters(unsigned** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return set_error(BRASA_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return set_error(BRASA_ERR_LAUNCH, "device %d out of range", dev);
+    std::call_once(g_ctr_once[dev], [dev] {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_arrivals)) == hipSuccess)
+            g_ctr_base[dev] = static_cast<unsigned*>(p);
+    });
+    if (!g_ctr_base[dev]) return set_error(BRASA_ERR_LAUNCH, "decode: arrival counters not found");
+    const unsigned slot = g_next_slot.fetch_add(1, std::memory_order_relaxed) % kCounterSlots;
+    *out = g_ctr_base[dev] + (size_t)slot * kSlotCounters;
+    return BRASA_OK;
+}
+
 }  // namespace
 
-// Launch plan for a batch of sequences. Splits have one length `chunk` for every sequence (a
-// multiple of 32 keys and at least 128, so a sequence of lk keys has at most ceil(lk / 128)
-// splits and its partials fit the reference's decode_partials_len(hq, lk) floats), chosen so that
-// about BRASA_DECODE_WGS workgroups (default 256 = one per CU) cover the batch.
-// f16 caches: the most head groups per workgroup (4, 2, 1) that still reach that many
-// workgroups, each head group read by 8 / hpw waves (4 waves for one head group when a split has
-// at most 4 blocks). Other caches: up to kMaxWaves head groups, one wave each.
-// The plan depends only on the lengths and head counts, so results are reproducible bit for bit.
-Plan decode_plan(const int* lk, int n, int ngroups, int kv) {
-    const char* env = getenv("BRASA_DECODE_WGS");
-    const long long target = env && atoi(env) > 0 ? atoi(env) : 256;
-    long long total = 0, max_splits = 0;
+// Split length for `keys` keys spread over about kTargetWgs / ngroups splits: a multiple of 32
+// keys and at least 128 keys, so a sequence of lk keys has at most ceil(lk / 128) splits and its
+// partials fit the reference's decode_partials_len(hq, lk).
+static long long split_chunk(long long keys, int ngroups) {
+    const int target = ngroups >= kTargetWgs ? 1 : kTargetWgs / ngroups;
+    long long chunk = (keys + target - 1) / target;
+    chunk = (chunk + kBlock - 1) / kBlock * kBlock;
+    return chunk < kMinChunk ? kMinChunk : chunk;
+}
+
+// Launch plan: head groups per workgroup (HPW) and one split length for every sequence of the
+// launch. Workgroups that read several adjacent KV heads load the HBM channels evenly (with one
+// KV head per workgroup, the heads whose rows sit on the slower channels arrive ~2 us late at
+// 16K keys), but each merge group then has HPW * G query heads; the plan takes the largest HPW
+// whose merge (query heads x splits of the longest sequence) stays within the bounds above,
+// with the split length set for ~kTargetWgs workgroups. f32 caches use one head group per workgroup.
+// A function of the lengths and head counts only, so a call's result never depends on anything
+// else.
+DecodePlan decode_plan(const int* lk, int n, int ngroups, int G, int kv) {
+    long long total = 0, lk_max = 0;
     for (int i = 0; i < n; ++i) {
         total += lk[i];
-        max_splits += (lk[i] + kMinChunk - 1) / kMinChunk;
+        lk_max = std::max<long long>(lk_max, lk[i]);
     }
-    Plan p{0, 1, 1, 4};
-    int per_wg = 1;  // head groups per workgroup
-    if (kv == BRASA_KV_F16 || kv == BRASA_KV_Q8_0) {
-        int hpw = 4;
-        while (hpw > 1 && max_splits * ((ngroups + hpw - 1) / hpw) < target) hpw >>= 1;
-        const char* fh = getenv("BRASA_DECODE_HPW");
-        if (fh && (atoi(fh) == 1 || atoi(fh) == 2 || atoi(fh) == 4)) hpw = atoi(fh);
-        p.hpw = per_wg = hpw;
-    } else {
-        int waves = kMaxWaves;
-        while (waves > 1 && max_splits * ((ngroups + waves - 1) / waves) < target) waves >>= 1;
-        p.waves = per_wg = waves;
+    for (int hpw = 4; hpw >= 1; hpw >>= 1) {
+        if (hpw > 1 && (kv == BRASA_KV_F32 || hpw * G > kMaxMergeHeads || hpw > ngroups)) continue;
+        const int rows = (ngroups + hpw - 1) / hpw;
+        const long long chunk = split_chunk(total, rows);
+        const long long splits = (lk_max + chunk - 1) / chunk;
+        const long long work = splits * hpw * G;
+        if (hpw == 1 || work <= kMergeWorkSmall || (chunk >= kLongChunk && work <= kMergeWorkLong))
+            return DecodePlan{(int)chunk, (int)splits, hpw};
     }
-    const long long rows = (ngroups + per_wg - 1) / per_wg;
-    long long splits = (target + rows - 1) / rows;
-    if (splits < 1) splits = 1;
-    long long chunk = (total + splits - 1) / splits;
-    chunk = (chunk + kBlock - 1) / kBlock * kBlock;
-    if (chunk < kMinChunk) chunk = kMinChunk;
-    for (int i = 0; i < n; ++i) {  // at most kMaxSplits splits per sequence
-        const long long need = ((long long)lk[i] + kMaxSplits - 1) / kMaxSplits;
-        if (chunk < need) chunk = (need + kBlock - 1) / kBlock * kBlock;
-    }
-    p.chunk = (int)chunk;
-    if (kv == BRASA_KV_F16 || kv == BRASA_KV_Q8_0) p.ks = (p.hpw == 1 && chunk <= 4 * kBlock) ? 4 : 8 / p.hpw;
-    return p;
+    return DecodePlan{kMinChunk, 1, 1};  // not reached
 }
 
 int decode_batch_launch(const float* q, const void* const* k, const void* const* v,
@@ -1266,12 +1260,14 @@ int decode_batch_launch(const float* q, const void* const* k, const void* const*
     const int group = hq / hkv;
     const int G = per_head ? 1 : group;
     const int ngroups = per_head ? hq : hkv;
-    const Plan plan = decode_plan(lk, n, ngroups, kv);
-    const int chunk = plan.chunk;
     const size_t oelem = o_f16 ? 2 : 4;
+    // sequences per launch: the descriptor array and the counter slot bound it
+    const int per_launch = std::min(kMaxSeqs, std::max(1, kSlotCounters / ngroups));
+    if (ngroups > kSlotCounters)
+        return set_error(BRASA_ERR_SHAPE, "decode: %d head groups exceed %d", ngroups, kSlotCounters);
     size_t part_off = 0;
-    for (int b0 = 0; b0 < n; b0 += kMaxSeqs) {
-        const int nb = min(kMaxSeqs, n - b0);
+    for (int b0 = 0; b0 < n; b0 += per_launch) {
+        const int nb = std::min(per_launch, n - b0);
         DecodeArgs<kMaxSeqs> a;
         memset(&a, 0, sizeof(a));
         a.q = q + (size_t)b0 * hq * kDim;
@@ -1282,39 +1278,29 @@ int decode_batch_launch(const float* q, const void* const* k, const void* const*
         a.hkv = hkv;
         a.group = group;
         a.ngroups = ngroups;
-        a.chunk = chunk;
         a.nseq = nb;
         a.scale = 1.0f / sqrtf(static_cast<float>(kDim));
-        ReduceArgs ra;
-        memset(&ra, 0, sizeof(ra));
-        ra.part = partials;
-        ra.o = a.o;
-        ra.o_f16 = o_f16;
-        ra.hq = hq;
-        ra.nseq = nb;
+        int st = arrival_counters(&a.ctr);
+        if (st != BRASA_OK) return st;
+        // one split length for the launch (a sequence's splits never exceed ceil(lk / 128))
+        const DecodePlan plan = decode_plan(lk + b0, nb, ngroups, G, kv);
+        const long long chunk = plan.chunk;
         int col = 0;
-        bool any_multi = false;
         for (int i = 0; i < nb; ++i) {
             SeqDesc& d = a.seq[i];
+            const DecodePlan p{(int)chunk, (int)((lk[b0 + i] + chunk - 1) / chunk), plan.hpw};
             d.k = static_cast<const uint8_t*>(k[b0 + i]);
             d.v = static_cast<const uint8_t*>(v[b0 + i]);
             d.lk = lk[b0 + i];
-            d.splits = (d.lk + chunk - 1) / chunk;
+            d.chunk = p.chunk;
+            d.splits = p.splits;
             d.split0 = col;
             d.part_off = part_off;
             col += d.splits;
             part_off += (size_t)hq * d.splits * (kDim + 2);
-            ra.splits[i] = d.splits;
-            ra.part_off[i] = d.part_off;
-            any_multi |= d.splits > 1;
         }
-        int st = nb == 1 ? launch_kv(one_seq(a), kv, G, plan, stream)
-                         : launch_kv(a, kv, G, plan, stream);
-        if (st != BRASA_OK) return st;
-        if (!any_multi) continue;
-        hipLaunchKernelGGL(decode_reduce_kernel, dim3(hq, kDim / kRedDims, nb), dim3(kRedThreads),
-                           0, stream, ra);
-        st = check_launch("decode_reduce_kernel");
+        st = nb == 1 ? launch_kv(one_seq(a), kv, G, plan.hpw, col, stream)
+                     : launch_kv(a, kv, G, plan.hpw, col, stream);
         if (st != BRASA_OK) return st;
     }
     return BRASA_OK;
