@@ -43,6 +43,7 @@ SYMBOLS = {
     "brasa_dequantize_kv_q8": (INT, [VP, VP, SZ, VP]),
     "brasa_decode_attention_lanes": (INT, [VP, VP, VP, VP, SZ, VP, INT, AttnShapeC, VP]),
     "brasa_decode_attention": (INT, [VP, VP, VP, VP, SZ, VP, INT, AttnShapeC, VP]),
+    "brasa_decode_attention_lanes_noalloc": (INT, [VP, VP, VP, VP, INT, AttnShapeC, VP]),
     "brasa_decode_batch_partials_len": (SZ, [SZ, VP, SZ]),
     "brasa_decode_attention_batch": (INT, [VP, VP, VP, VP, SZ, VP, SZ, VP, INT, SZ, SZ, SZ, INT,
                                            VP]),

@@ -17,6 +17,8 @@ int fill_u8_launch(void* dst, uint8_t value, size_t bytes, hipStream_t stream);
 int fill_normal_launch(float* out, size_t n, uint64_t seed, float scale, hipStream_t stream);
 int decode_launch(const float* q, const void* k, const void* v, float* partials, void* o,
                   int o_f16, int hq, int hkv, int lk, int kv, bool per_head, hipStream_t stream);
+int decode_noalloc_launch(const float* q, const void* k, const void* v, void* o, int o_f16,
+                          int hq, int hkv, int lk, int kv, hipStream_t stream);
 int rms_norm_launch(const float* x, const float* w, float* out, size_t rows, size_t n, float eps,
                     hipStream_t stream);
 int rope_neox_launch(float* x, const float* cos_t, const float* sin_t, size_t tokens,
@@ -126,9 +128,11 @@ int brasa_dequantize_kv_q8(const void* src, float* dst, size_t rows, void* strea
     return dequant_q8_launch(src, dst, rows, as_stream(stream));
 }
 
+// Shape checks of the decode entry points (lib.rs:1074-1080 / 1128-1135). partials == nullptr
+// with noalloc: the library's fixed scratch array is used instead of the caller's.
 static int decode_common(const float* q, const void* k, const void* v, float* partials,
                          size_t partials_len, void* o, int o_dtype, brasa_attn_shape s,
-                         void* stream, bool per_head) {
+                         void* stream, bool per_head, bool noalloc = false) {
     g_err[0] = 0;
     if (!valid_kv(s.kv)) return set_error(BRASA_ERR_ARG, "decode: invalid kv type %d", s.kv);
     if (o_dtype != BRASA_OUT_F32 && o_dtype != BRASA_OUT_F16)
@@ -142,13 +146,17 @@ static int decode_common(const float* q, const void* k, const void* v, float* pa
     if (s.hq > kMaxHeads || s.pos0 + 1 > kMaxPositions)
         return set_error(BRASA_ERR_SHAPE, "decode: shape too large");
     const size_t lk = s.pos0 + 1;
-    if (partials_len < brasa_decode_partials_len(s.hq, lk))
+    if (!noalloc && partials_len < brasa_decode_partials_len(s.hq, lk))
         return set_error(BRASA_ERR_SCRATCH, "decode scratch too small (%zu < %zu floats)",
                          partials_len, brasa_decode_partials_len(s.hq, lk));
     if (!per_head && !brasa_gqa_supported(s.hq, s.hkv))
         return set_error(BRASA_ERR_UNSUPPORTED,
                          "decode_attention_lanes: GQA group %zu not compiled", s.hq / s.hkv);
-    if (!q || !k || !v || !partials || !o) return set_error(BRASA_ERR_ARG, "decode: null pointer");
+    if (!q || !k || !v || (!partials && !noalloc) || !o)
+        return set_error(BRASA_ERR_ARG, "decode: null pointer");
+    if (noalloc)
+        return decode_noalloc_launch(q, k, v, o, o_dtype == BRASA_OUT_F16, (int)s.hq, (int)s.hkv,
+                                     (int)lk, s.kv, as_stream(stream));
     return decode_launch(q, k, v, partials, o, o_dtype == BRASA_OUT_F16, (int)s.hq, (int)s.hkv,
                          (int)lk, s.kv, per_head, as_stream(stream));
 }
@@ -157,6 +165,11 @@ int brasa_decode_attention_lanes(const float* q, const void* k, const void* v, f
                                  size_t partials_len, void* o, int o_dtype,
                                  brasa_attn_shape shape, void* stream) {
     return decode_common(q, k, v, partials, partials_len, o, o_dtype, shape, stream, false);
+}
+
+int brasa_decode_attention_lanes_noalloc(const float* q, const void* k, const void* v, void* o,
+                                         int o_dtype, brasa_attn_shape shape, void* stream) {
+    return decode_common(q, k, v, nullptr, 0, o, o_dtype, shape, stream, false, true);
 }
 
 int brasa_decode_attention(const float* q, const void* k, const void* v, float* partials,

@@ -76,6 +76,11 @@ constexpr int kSlotCounters = 8192;
 constexpr int kCounterSlots = 64;
 __device__ unsigned g_arrivals[kCounterSlots * kSlotCounters];
 
+// Split partials of brasa_decode_attention_lanes_noalloc: one fixed array per device, used in
+// place of the caller's scratch (BRASA_DECODE_NOALLOC_FLOATS floats; a call needs
+// hq * splits * 130 of them). Every call on a device shares it.
+static __device__ __align__(256) float scratch[BRASA_DECODE_NOALLOC_FLOATS];
+
 struct SeqDesc {
     const uint8_t* k;     // layer cache base of this sequence
     const uint8_t* v;
@@ -1304,6 +1309,36 @@ int decode_batch_launch(const float* q, const void* const* k, const void* const*
         if (st != BRASA_OK) return st;
     }
     return BRASA_OK;
+}
+
+// Device address of `scratch`, looked up once per device with that device current.
+float* g_scratch_ptr[kMaxDevices];
+std::once_flag g_scratch_once[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+int decode_noalloc_launch(const float* q, const void* k, const void* v, void* o, int o_f16,
+                          int hq, int hkv, int lk, int kv, hipStream_t stream) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return set_error(BRASA_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return set_error(BRASA_ERR_LAUNCH, "device %d out of range", dev);
+    std::call_once(g_scratch_once[dev], [dev] {
+        void* p = nullptr;
+        g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (g_scratch_err[dev] == hipSuccess) g_scratch_ptr[dev] = static_cast<float*>(p);
+    });
+    if (g_scratch_err[dev] != hipSuccess || !g_scratch_ptr[dev])
+        return set_error(BRASA_ERR_LAUNCH, "decode_noalloc: hipGetSymbolAddress(scratch): %s",
+                         hipGetErrorString(g_scratch_err[dev]));
+    const int G = hq / hkv;
+    const DecodePlan plan = decode_plan(&lk, 1, hkv, G, kv);
+    const size_t need = (size_t)hq * plan.splits * (kDim + 2);
+    if (need > (size_t)BRASA_DECODE_NOALLOC_FLOATS)
+        return set_error(BRASA_ERR_SCRATCH,
+                         "decode_noalloc: needs %zu scratch floats, the fixed array holds %d "
+                         "(hq %d, %d keys)", need, BRASA_DECODE_NOALLOC_FLOATS, hq, lk);
+    return decode_batch_launch(q, &k, &v, &lk, 1, g_scratch_ptr[dev], o, o_f16, hq, hkv, kv, false,
+                               stream);
 }
 
 int decode_launch(const float* q, const void* k, const void* v, float* partials, void* o,

@@ -167,6 +167,14 @@ class Kernels:
                                                  plen, _ptr(o), int(out), shape.c(),
                                                  _stream(stream or self.stream)))
 
+    def decode_attention_lanes_noalloc(self, q, k, v, o, shape: AttnShape,
+                                       out: OutDType = OutDType.F32, stream=None) -> None:
+        """decode_attention_lanes with the split partials in the library's fixed device array
+        (no caller scratch, no allocation; calls overlapping on one GPU race)."""
+        check(lib().brasa_decode_attention_lanes_noalloc(_ptr(q), _ptr(k), _ptr(v), _ptr(o),
+                                                         int(out), shape.c(),
+                                                         _stream(stream or self.stream)))
+
     def decode_attention(self, q, k, v, partials: DeviceBuffer, o, shape: AttnShape,
                          out: OutDType = OutDType.F32, stream=None,
                          partials_len: int | None = None) -> None:

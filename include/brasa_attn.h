@@ -127,6 +127,22 @@ int brasa_decode_attention_lanes(const float* q, const void* k, const void* v, f
                                  brasa_attn_shape shape, void* stream);
 
 /*
+ * No counterpart in the reference. brasa_decode_attention_lanes without the caller's scratch,
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): the split partials live in a fixed array inside the
+ * library, BRASA_DECODE_NOALLOC_FLOATS floats (4 MiB) per device, held until the process ends.
+ * A call needs hq * splits * 130 floats, where the launch plan keeps splits <= 256 / hkv (with
+ * 8 KV heads: 32 splits, 133,120 floats for hq 32, at any length); a call needing more fails
+ * with BRASA_ERR_SCRATCH. The call allocates nothing.
+ * Every call on one device shares the array: calls that overlap on one GPU (different streams
+ * without ordering) race and give wrong results. Same results, bit for bit, as
+ * brasa_decode_attention_lanes on the same arguments.
+ */
+#define BRASA_DECODE_NOALLOC_FLOATS (1 << 20)
+int brasa_decode_attention_lanes_noalloc(const float* q, const void* k, const void* v, void* o,
+                                         int o_dtype, brasa_attn_shape shape, void* stream);
+
+/*
  * Kernels::decode_attention (lib.rs:1056-1103; decode_attention.metal:15-84): same contract as
  * brasa_decode_attention_lanes, one query head per workgroup, for any hq multiple of hkv (the
  * reference's fallback for groups outside {1, 2, 4, 8}).
