@@ -26,7 +26,8 @@ sys.path.insert(0, ROOT)
 
 import numpy as np  # noqa: E402
 
-from brasa_amd import (AttnShape, Kernels, KvType, OutDType, RopeTable,  # noqa: E402
+from brasa_amd import (AttnShape, Kernels, KvType, OutDType, PrefillPrecision,  # noqa: E402
+                       RopeTable,
                        decode_batch_partials_len,
                        decode_partials_len)  # noqa: E402
 from brasa_amd.device import (DeviceBuffer, Event, Stream, device_name, fill_normal,  # noqa: E402
@@ -165,27 +166,42 @@ def bench_ragged(k, stream, steps, warmup, seed=12345):
             "GBps_batched": total / tb / 1e9}
 
 
-def bench_prefill(k, stream, tokens, pos0, kv, steps, warmup, seed=3):
+def bench_prefill(k, stream, tokens, pos0, kv, steps, warmup, seed=3,
+                  precision=PrefillPrecision.F16):
+    """Causal prefill of `tokens` queries at positions pos0.. over a cache of ceil64(pos0 +
+    tokens) positions. As BASELINE.json config 4 describes the inputs: Q and K are N(0, 1) put
+    through per-head RMSNorm (weight 1, eps 1e-6) and RoPE-NeoX (theta 1e6) at their positions
+    by the library's own kernels, V is N(0, 1); K and V are stored in the cache type."""
     lk = pos0 + tokens
     cap = (lk + 63) // 64 * 64
     n = cap * HKV * DIM
-    tmp = DeviceBuffer(4 * max(n, tokens * HQ * DIM))
+    table = RopeTable(1e6, DIM, cap)
+    ones = DeviceBuffer.from_array(np.ones(DIM, np.float32))
+    tmp = DeviceBuffer(4 * n)
     kb, vb = DeviceBuffer(kv.bytes(n)), DeviceBuffer(kv.bytes(n))
     fill_normal(tmp, n, seed, 1.0, stream)
+    k.rms_norm(tmp, ones, tmp, cap * HKV, DIM, 1e-6, stream)
+    k.rope_neox(tmp, table, cap, HKV, DIM, 0, stream)
     k.store_kv(kv, tmp, kb, n, stream)
     fill_normal(tmp, n, seed + 1, 1.0, stream)
     k.store_kv(kv, tmp, vb, n, stream)
     q = DeviceBuffer(4 * tokens * HQ * DIM)
     fill_normal(q, tokens * HQ * DIM, seed + 2, 1.0, stream)
-    o = DeviceBuffer(2 * tokens * HQ * DIM)
+    k.rms_norm(q, ones, q, tokens * HQ, DIM, 1e-6, stream)
+    k.rope_neox(q, table, tokens, HQ, DIM, pos0, stream)
+    obytes = 4 if precision == PrefillPrecision.F32 else 2
+    o = DeviceBuffer(obytes * tokens * HQ * DIM)
     stream.synchronize()
     tmp.free()
     shape = AttnShape(tokens, HQ, HKV, DIM, pos0, kv)
-    t = time_steps(lambda s: k.flash_attention(q, kb, vb, o, shape, s), stream, steps, warmup)
+    t = time_steps(lambda s: k.flash_attention_with(q, kb, vb, o, shape, precision, s), stream,
+                   steps, warmup)
     tf = prefill_flops(tokens, pos0) / t / 1e12
-    log(f"prefill kv={kv.name_str} T={tokens} pos0={pos0}: {t * 1e6:.1f} µs, {tf:.1f} TFLOP/s")
-    for b in (kb, vb, q, o):
+    log(f"prefill kv={kv.name_str} {precision.name} T={tokens} pos0={pos0}: {t * 1e6:.1f} µs, "
+        f"{tf:.1f} TFLOP/s")
+    for b in (kb, vb, q, o, ones):
         b.free()
+    table.free()
     return {"us": t * 1e6, "TFLOPs": tf, "flop": prefill_flops(tokens, pos0),
             "frac_mfma_f16_peak": tf / MFMA_F16_PEAK_TFLOPS}, t
 
@@ -295,7 +311,13 @@ def profile_run(k: Kernels, stream: Stream, what: str) -> int:
     dst.free()
     decode_cases = {"decode": (16384, KvType.F16), "decode_q8": (16384, KvType.Q8_0),
                     "decode_4k": (4096, KvType.F16), "decode_32k": (32768, KvType.F16)}
-    prefill_cases = {"prefill": (2048, 0), "prefill_8k": (8192, 0), "prefill_chunk": (512, 16384)}
+    f16, q8, pf32 = KvType.F16, KvType.Q8_0, PrefillPrecision.F16_PF32
+    prefill_cases = {"prefill": (2048, 0, f16, PrefillPrecision.F16),
+                     "prefill_8k": (8192, 0, f16, PrefillPrecision.F16),
+                     "prefill_chunk": (512, 16384, f16, PrefillPrecision.F16),
+                     "prefill_pf32": (2048, 0, f16, pf32),
+                     "prefill_q8": (2048, 0, q8, PrefillPrecision.F16),
+                     "prefill_q8_chunk": (512, 16384, q8, PrefillPrecision.F16)}
     if what in decode_cases:
         lk, kv = decode_cases[what]
         layers = DecodeLayers(k, lk, kv, stream)
@@ -306,8 +328,8 @@ def profile_run(k: Kernels, stream: Stream, what: str) -> int:
     elif what == "decode_ragged":
         bench_ragged(k, stream, 3, 1)
     else:
-        tokens, pos0 = prefill_cases[what]
-        bench_prefill(k, stream, tokens, pos0, KvType.F16, 10, 2)
+        tokens, pos0, kv, prec = prefill_cases[what]
+        bench_prefill(k, stream, tokens, pos0, kv, 10, 2, precision=prec)
     log(f"profile run '{what}' done")
     return 0
 
@@ -321,7 +343,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile", choices=("decode", "decode_q8", "decode_4k", "decode_32k",
                                           "decode_ragged", "prefill", "prefill_8k",
-                                          "prefill_chunk"),
+                                          "prefill_chunk", "prefill_pf32", "prefill_q8",
+                                          "prefill_q8_chunk"),
                     help="short fixed run for rocprofv3 (kernel trace / counters), no JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -351,6 +374,11 @@ def main() -> int:
                                                                  20, 3)
         extra_prefill["T8192"], _ = bench_prefill(k, stream, 8192, 0, KvType.F16, 10, 2)
         extra_prefill["T512_pos16384"], _ = bench_prefill(k, stream, 512, 16384, KvType.F16, 10, 2)
+        extra_prefill["T2048_f16_pf32"], _ = bench_prefill(
+            k, stream, 2048, 0, KvType.F16, 20, 3, precision=PrefillPrecision.F16_PF32)
+        extra_prefill["q8_T2048"], _ = bench_prefill(k, stream, 2048, 0, KvType.Q8_0, 10, 2)
+        extra_prefill["q8_T512_pos16384"], _ = bench_prefill(k, stream, 512, 16384, KvType.Q8_0,
+                                                             10, 2)
     cpu = None if args.no_cpu else cpu_baseline()
 
     per_layer_s = head["us_per_layer"] / 1e6
@@ -379,7 +407,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic(),
-                     "kernel": "decode attention (split kernel + reduce kernel) per layer"},
+                     "kernel": "decode_f16_kernel (splits merged in the same launch), per layer"},
         "roofline_prefill": {"bound": "mfma", "achieved": round(pre2k["TFLOPs"], 1),
                              "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                              "frac": round(pre2k["TFLOPs"] / MFMA_F16_PEAK_TFLOPS, 4)},

@@ -33,6 +33,7 @@ int decode_batch_launch(const float* q, const void* const* k, const void* const*
                         int hkv, int kv, bool per_head, hipStream_t stream);
 int prefill_launch(const float* q, const void* k, const void* v, void* o, int tokens, int hq,
                    int hkv, int pos0, int kv, int precision, hipStream_t stream);
+void prefill_set_layout(int variant, int pair);
 
 namespace {
 thread_local char g_err[512] = "";
@@ -231,6 +232,11 @@ int brasa_flash_attention_with(const float* q, const void* k, const void* v, voi
         return set_error(BRASA_ERR_SHAPE, "hq must be a multiple of hkv");
     if (s.hq > kMaxHeads || s.pos0 + s.tokens + BRASA_KV_ALIGN > kMaxPositions)
         return set_error(BRASA_ERR_SHAPE, "flash_attention: shape too large");
+    // lib.rs:1227-1231: outside the compiled GQA groups only the f32 kernel exists
+    if (!brasa_gqa_supported(s.hq, s.hkv) && precision != BRASA_PREFILL_F32)
+        return set_error(BRASA_ERR_UNSUPPORTED,
+                         "flash_attention: without a compiled GQA group (%zu) attention is f32 only",
+                         s.hq / s.hkv);
     if (s.tokens == 0) return BRASA_OK;
     if (!q || !k || !v || !o) return set_error(BRASA_ERR_ARG, "flash_attention: null pointer");
     return prefill_launch(q, k, v, o, (int)s.tokens, (int)s.hq, (int)s.hkv, (int)s.pos0, s.kv,
@@ -293,6 +299,14 @@ int brasa_qk_norm_rope_store(int kv, float* q, float* k, const float* v, const f
     return qk_norm_rope_store_launch(kv, q, k, v, q_norm, k_norm, eps, table.cos, table.sin,
                                      k_dst, v_dst, s.tokens, s.hq, s.hkv, s.pos0,
                                      as_stream(stream));
+}
+
+int brasa_test_set_prefill_layout(int variant, int pair) {
+    g_err[0] = 0;
+    if (variant != 0 && variant != 1 && variant != 2 && variant != 4)
+        return set_error(BRASA_ERR_ARG, "prefill layout: variant %d (0, 1, 2 or 4)", variant);
+    prefill_set_layout(variant, pair ? 1 : 0);
+    return BRASA_OK;
 }
 
 const char* brasa_last_error(void) { return g_err; }

@@ -26,6 +26,7 @@
 //     by workgroup count: prefill_f16_kernel (8 waves, two key groups whose MFMA and softmax
 //     phases alternate; up to two workgroups per CU), prefill_f16_kernel4 (4 waves, two per CU)
 //     and prefill_f16_kernel4s (4 waves on 32-key stages, three per CU).
+#include <atomic>
 #include <type_traits>
 
 #include "common.hpp"
@@ -1117,21 +1118,21 @@ int launch(const PrefillArgs& a, hipStream_t stream) {
 // wave groups (T = 2048: 512 workgroups, 58 vs 63 µs for the others; T = 512 at pos0 16384: 128
 // workgroups, 269 vs 358 µs); from three per CU the 32-key-stage kernel with three workgroups per
 // CU (T = 4096: 156 vs 187 µs; T = 8192: 580 vs 631 µs); in between the four-wave kernel
-// (T = 2560: 76 vs 82 µs). BRASA_PREFILL_VARIANT=1, 2 or 4 forces one of them. The two-group
-// kernel pairs heavy and light query tiles when the pairs still fill every CU (T = 2048:
-// 57.0 vs 58.6 µs; at T = 1536 the 192 pairs leave CUs idle, 44 vs 39 µs);
-// BRASA_PREFILL_PAIR=0 turns pairing off.
+// (T = 2560: 76 vs 82 µs). The two-group kernel pairs heavy and light query tiles when the pairs
+// still fill every CU (T = 2048: 57.0 vs 58.6 µs; at T = 1536 the 192 pairs leave CUs idle,
+// 44 vs 39 µs). brasa_test_set_prefill_layout() forces a kernel or turns pairing off, for tests
+// that cover every kernel at small sizes; the product path never calls it.
+std::atomic<int> g_force_variant{0};  // 0: chosen by size; 1, 2, 4: the kernels above
+std::atomic<int> g_allow_pair{1};
+
 template <int HW, bool PS>
 int launch_f16(const PrefillArgs& a, hipStream_t stream) {
     const long long wgs = (long long)(a.hq / HW) * a.ntiles;
-    const char* ev = getenv("BRASA_PREFILL_VARIANT");  // read per call (tests switch it)
-    const int variant = ev ? atoi(ev) : 0;
+    const int variant = g_force_variant.load(std::memory_order_relaxed);
     const int pick = variant ? variant : wgs <= 2 * 256 ? 1 : wgs < 3 * 256 ? 2 : 4;
     if (pick == 1) {
-        const char* ep = getenv("BRASA_PREFILL_PAIR");
-        const int pair_env = ep ? atoi(ep) : 1;
         PrefillArgs b = a;
-        b.pair = pair_env && wgs >= 2 * 256;  // pairs still fill every CU
+        b.pair = g_allow_pair.load(std::memory_order_relaxed) && wgs >= 2 * 256;
         const int rows = b.pair ? (a.ntiles + 1) / 2 : a.ntiles;
         hipLaunchKernelGGL((prefill_f16_kernel<HW, PS>), dim3(a.hq / HW, rows),
                            dim3(2 * kThreads), 0, stream, b);
@@ -1173,6 +1174,11 @@ int launch_kv(PrefillArgs& a, int precision, hipStream_t stream) {
 }
 
 }  // namespace
+
+void prefill_set_layout(int variant, int pair) {
+    g_force_variant.store(variant, std::memory_order_relaxed);
+    g_allow_pair.store(pair, std::memory_order_relaxed);
+}
 
 int prefill_launch(const float* q, const void* k, const void* v, void* o, int tokens, int hq,
                    int hkv, int pos0, int kv, int precision, hipStream_t stream) {

@@ -138,6 +138,10 @@ class RopeTable:
     def c(self) -> RopeTableC:
         return RopeTableC(self.cos.ptr, self.sin.ptr, self.dim, self.max_pos)
 
+    def free(self) -> None:
+        self.cos.free()
+        self.sin.free()
+
 
 class Kernels:
     """Attention methods of ``brasa_kernels::Kernels`` on gfx950.

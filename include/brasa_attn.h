@@ -121,6 +121,9 @@ int brasa_dequantize_kv_q8(const void* src, float* dst, size_t rows, void* strea
  * `o_dtype`. partials: caller scratch of partials_len floats, at least
  * brasa_decode_partials_len(hq, pos0 + 1). Requires tokens == 1, dim == 128 and
  * hq / hkv in {1, 2, 4, 8} (BRASA_ERR_UNSUPPORTED otherwise, where the reference panics).
+ * The result bits depend only on q, the cache rows and lk: the launch layout is a function of
+ * lk and the head counts (no tuning knob), and the split merge runs in a fixed order, as the
+ * reference requires of every launch width (crates/kernels/tests/launch.rs:119-168).
  */
 int brasa_decode_attention_lanes(const float* q, const void* k, const void* v, float* partials,
                                  size_t partials_len, void* o, int o_dtype,
@@ -157,8 +160,11 @@ int brasa_decode_attention(const float* q, const void* k, const void* v, float* 
  * would otherwise issue one call per sequence). One launch of the split kernel (and one of the
  * merge) covers n sequences: sequence i has one query q[i] (q: [n, hq, 128] f32), its own layer
  * caches k[i] / v[i] (HOST arrays of device pointers, same layout as decode_attention_lanes) and
- * lk[i] >= 1 keys (HOST array). o: [n, hq, 128] in o_dtype. Each sequence's result equals
- * brasa_decode_attention_lanes on it alone. Scratch: partials_len >=
+ * lk[i] >= 1 keys (HOST array). o: [n, hq, 128] in o_dtype. Each sequence's result agrees with
+ * brasa_decode_attention_lanes on it alone to the decode tolerance, not bit for bit: a launch
+ * cuts every sequence into splits of one length chosen from the batch's total keys, so the split
+ * boundaries (and the f32 rounding of the merge) differ from the single-sequence call's. A
+ * single-sequence call's result depends only on its inputs and lk. Scratch: partials_len >=
  * brasa_decode_batch_partials_len(hq, lk, n) floats. Requires dim == 128 and a GQA group in
  * {1, 2, 4, 8}.
  */
@@ -175,7 +181,8 @@ int brasa_decode_attention_batch(const float* q, const void* const* k, const voi
  * pos0 + tokens are masked; they must be finite). o: [tokens, hq, 128], f16 bits for
  * BRASA_PREFILL_F16 / BRASA_PREFILL_F16_PF32 (Q*scale rounded to f16 as the reference does,
  * fp32 softmax and accumulation) or f32 for BRASA_PREFILL_F32. Requires dim == 128 and
- * hq % hkv == 0.
+ * hq % hkv == 0; when hq / hkv is not in {1, 2, 4, 8} only BRASA_PREFILL_F32 is accepted
+ * (BRASA_ERR_UNSUPPORTED otherwise), as the reference asserts (lib.rs:1227-1231).
  */
 int brasa_flash_attention_with(const float* q, const void* k, const void* v, void* o,
                                brasa_attn_shape shape, int precision, void* stream);
@@ -230,6 +237,16 @@ int brasa_rope_neox(float* x, brasa_rope_table_view table, size_t tokens, size_t
 int brasa_qk_norm_rope_store(int kv, float* q, float* k, const float* v, const float* q_norm,
                              const float* k_norm, float eps, brasa_rope_table_view table,
                              void* k_dst, void* v_dst, brasa_attn_shape shape, void* stream);
+
+/*
+ * Test hook (no counterpart in the reference; a production caller never needs it). The prefill
+ * kernel for BRASA_KV_F16 is chosen by workgroup count; tests force each of the three kernels at
+ * small sizes with variant 1 (two key groups per workgroup), 2 (four waves) or 4 (four waves,
+ * 32-key stages), and 0 restores the choice by size. pair = 0 stops the two-group kernel from
+ * pairing heavy and light query tiles (the results are identical either way). Process-wide; set
+ * it only while no prefill call is being enqueued on another thread.
+ */
+int brasa_test_set_prefill_layout(int variant, int pair);
 
 /* Description of the last error on this thread ("" if none). */
 const char* brasa_last_error(void);

@@ -99,6 +99,11 @@ def test_prefill_and_store_asserts_without_device():
                                           AttnShape(16, 30, 8, 128, 0, KvType.F16))) == 1
     assert _err(lambda: k.flash_attention_with(fake, fake, fake, fake,
                                                AttnShape(16, 32, 8, 128, 0, KvType.F16), 7)) == 5
+    # lib.rs:1227-1231: a group outside {1, 2, 4, 8} has only the f32 kernel
+    for prec in (0, 2):
+        assert _err(lambda: k.flash_attention_with(fake, fake, fake, fake,
+                                                   AttnShape(16, 24, 8, 128, 0, KvType.F16),
+                                                   prec)) == 3
     assert _err(lambda: k.store_kv(KvType.Q8_0, fake, fake, 100)) == 1
     assert _err(lambda: k.store_kv(9, fake, fake, 128)) == 5
     # zero-size calls are no-ops
@@ -155,6 +160,17 @@ def test_rope_table_host_matches_oracle():
     # position 0 is the identity; p * inv_freq for i = 0 is p radians
     assert np.all(cos[0] == 1.0) and np.all(sin[0] == 0.0)
     assert cos[1000, 0] == np.float32(np.cos(1000.0))
+
+
+def test_decode_noalloc_asserts_without_device():
+    k = Kernels()
+    fake = 0x1000
+    assert _err(lambda: k.decode_attention_lanes_noalloc(
+        fake, fake, fake, fake, AttnShape(2, 32, 8, 128, 5, KvType.F16))) == 1
+    assert _err(lambda: k.decode_attention_lanes_noalloc(
+        fake, fake, fake, fake, AttnShape(1, 24, 8, 128, 5, KvType.F16))) == 3
+    assert _err(lambda: k.decode_attention_lanes_noalloc(
+        fake, fake, 0, fake, AttnShape(1, 32, 8, 128, 5, KvType.F16))) == 5
 
 
 def test_decode_batch_asserts_without_device():

@@ -101,6 +101,15 @@ def test_decode_launch_seed78_and_determinism(kv):
         a = run_decode(k, "lanes", q, cache, HQ, HKV, lk - 1)
         b = run_decode(k, "lanes", q, cache, HQ, HKV, lk - 1)
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        # the same bits from scratch holding garbage and through the batched entry point with
+        # one sequence (launch.rs:119-168: no launch choice changes the result)
+        gq = DeviceBuffer.from_array(q)
+        part = DeviceBuffer.from_array(np.full(decode_partials_len(HQ, lk), np.nan, np.float32))
+        o = DeviceBuffer(HQ * DIM * 4)
+        k.decode_attention_batch(gq, [cache.kbuf], [cache.vbuf], [lk], part, o, HQ, HKV, kv)
+        synchronize()
+        c = o.download(np.float32).reshape(HQ, DIM)
+        assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
         want, vmax = oracle.attention(q, cache.k[: lk * HKV * DIM], cache.v[: lk * HKV * DIM],
                                       1, HQ, HKV, DIM, lk - 1)
         assert oracle.worst(a, want, vmax) <= 1e-5

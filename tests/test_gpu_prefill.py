@@ -16,6 +16,7 @@ import pytest
 
 import oracle
 from brasa_amd import AttnShape, Kernels, KvType, PrefillPrecision
+from brasa_amd._lib import check, lib
 from brasa_amd.device import DeviceBuffer, synchronize
 from gpu_util import DIM, HKV, HQ, KvPair, bars
 
@@ -85,6 +86,8 @@ def test_flash_other_groups(hq, hkv):
         o32 = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F32)
         raw, vmax = oracle.attention(q, cache.k, cache.v, tokens, hq, hkv, DIM, pos0)
         assert oracle.worst(o32, raw, vmax) <= 1e-5
+        if (hq // hkv) not in (1, 2, 4, 8):
+            continue  # f32 only outside the GQA groups (lib.rs:1227-1231; tests/test_abi.py)
         oh = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
         ref16, _ = oracle.attention(q, cache.k, cache.v, tokens, hq, hkv, DIM, pos0, q16=True)
         a, r = bars(oracle.f16_to_f32(oh), ref16)
@@ -164,7 +167,7 @@ def test_flash_stage_ring_variant():
         assert w <= 1e-5, (t0, w)
 
 
-def test_flash_paired_tiles(monkeypatch):
+def test_flash_paired_tiles():
     # 64 query heads (group 4) x 33 tiles of 32 tokens = 528 workgroups with the two-group
     # kernel forced: heavy and light tiles run in pairs (y, 32 - y) and the middle tile 16 alone.
     # The rows checked cover a heavy tile, the unpaired middle tile and a light tile; the same
@@ -176,14 +179,17 @@ def test_flash_paired_tiles(monkeypatch):
     cap = (lk + 63) // 64 * 64
     q = rng.vec(tokens * hq * DIM, 2.0)
     cache = KvPair(KvType.F16, rng.vec(cap * hkv * DIM, 2.0), rng.vec(cap * hkv * DIM, 3.0))
-    monkeypatch.setenv("BRASA_PREFILL_VARIANT", "1")
-    _say(f"prefill paired F16 hq={hq} T={tokens} pos0={pos0}")
-    oh = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
-    _say(f"prefill paired F16_PF32 hq={hq} T={tokens} pos0={pos0}")
-    op = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16_PF32)
-    monkeypatch.setenv("BRASA_PREFILL_PAIR", "0")
-    _say(f"prefill unpaired F16 hq={hq} T={tokens} pos0={pos0}")
-    ou = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
+    try:
+        check(lib().brasa_test_set_prefill_layout(1, 1))
+        _say(f"prefill paired F16 hq={hq} T={tokens} pos0={pos0}")
+        oh = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
+        _say(f"prefill paired F16_PF32 hq={hq} T={tokens} pos0={pos0}")
+        op = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16_PF32)
+        check(lib().brasa_test_set_prefill_layout(1, 0))
+        _say(f"prefill unpaired F16 hq={hq} T={tokens} pos0={pos0}")
+        ou = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
+    finally:
+        check(lib().brasa_test_set_prefill_layout(0, 1))
     assert np.array_equal(oh, ou)
     for t0, t1 in [(0, 32), (512, 544), (1024, 1040)]:
         ref16, vmax = oracle.attention(q, cache.k, cache.v, tokens, hq, hkv, DIM, pos0,

@@ -280,3 +280,30 @@ def test_rms_norm_and_rope():
     t4 = t.reshape(3, 2, 2, 64)
     np.testing.assert_allclose(np.hypot(r[:, :, 0], r[:, :, 1]), np.hypot(t4[:, :, 0], t4[:, :, 1]),
                                rtol=1e-6)
+
+
+def test_rope_neox_rotation_closed_form():
+    """reference.rs:45-58 pinned by unit vectors, independently of the table: at position p,
+    e_i (i < 64) turns into (cos a, sin a) in slots (i, i + 64) and e_{i+64} into (-sin a, cos a),
+    a = p * theta^(-2 i / 128). A swapped sign or slot (rotation the other way) fails here."""
+    theta, dim, max_pos = 1e6, 128, 4096
+    c, s = oracle.rope_table(theta, dim, max_pos)
+    for pos0, tokens in [(1, 3), (1000, 2), (4090, 6)]:
+        for i in (0, 1, 17, 63):
+            for hi in (False, True):
+                x = np.zeros((tokens, 2, dim), np.float32)
+                x[:, 1, i + 64 if hi else i] = 1.0  # head 1 of 2; head 0 stays zero
+                y = oracle.rope_neox(x, tokens, 2, dim, pos0, c, s).reshape(tokens, 2, dim)
+                assert not y[:, 0].any()
+                for t in range(tokens):
+                    a = (pos0 + t) * theta ** (-(2 * i) / dim)
+                    ca, sa = math.cos(a), math.sin(a)
+                    want_lo, want_hi = (-sa, ca) if hi else (ca, sa)
+                    assert abs(y[t, 1, i] - want_lo) <= 1e-6 and abs(y[t, 1, i + 64] - want_hi) <= 1e-6
+                    others = np.delete(y[t, 1], [i, i + 64])
+                    assert not others.any()
+    # i = 0 at p = 1: one radian, counter-clockwise (sin 1 > 0 lands in the upper half)
+    x = np.zeros(dim, np.float32)
+    x[0] = 1.0
+    y = oracle.rope_neox(x, 1, 1, dim, 1, c, s)
+    assert y[64] > 0.84 and abs(y[0] - math.cos(1.0)) <= 1e-7
