@@ -57,6 +57,18 @@ __device__ __forceinline__ uint32_t q8_code(float x, float d) {
     return (uint32_t)(uint8_t)(int8_t)qv;
 }
 
+// 4 int8 codes (one dword) -> 4 exact f16 values: f16 bits 0x6400 | (code + 128) encode
+// 1024 + code + 128, minus 1152 (exact in f16 for these integers)
+__device__ __forceinline__ void codes4_to_f16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    const uint32_t x = w ^ 0x80808080u;
+    const uint32_t l = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);  // [64, b1, 64, b0]
+    const uint32_t h = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);  // [64, b3, 64, b2]
+    typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+    const half2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, l) + bias);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, h) + bias);
+}
+
 // ---- DPP / cross-lane helpers (wave64) ----------------------------------------------------
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {

@@ -924,6 +924,213 @@ prefill_f16_kernel4(PrefillArgs a) {
                  a.tokens, a.hq, h);
 }
 
+// ---- q8_0 cache, F16 precision ------------------------------------------------------------
+// prefill_f16_kernel4's work order and tile code, fed from a q8_0 cache: each wave loads its 16
+// rows of a 64-key stage (codes and the group scales) into registers one stage ahead, converts
+// every value to f16(code * scale) (the exact dequantised value rounded once, like Q * scale in
+// this precision; codes4_to_f16 gives the codes exactly, one packed f16 multiply the rounding)
+// and writes the f16 rows in the swizzled layouts the f16 kernels read, so the contraction runs
+// at one MFMA per product instead of the generic kernel's hi / lo splits.
+struct Q8Rows {
+    u32x4 kc[2], vc[2];   // 16 codes of rows r0, r0 + 8 (lane's 16-byte chunk)
+    uint32_t ks[2], vs[2];  // the f16 scale of the chunk's 32-group, per row (low half)
+};
+
+template <int HW>
+__global__ void __launch_bounds__(kThreads, 2)
+prefill_q8_kernel4(PrefillArgs a) {
+    constexpr int TPW = 32 * 4 / HW;
+    constexpr int RB = kQ8Row;
+    __shared__ __attribute__((aligned(16))) uint16_t s_k[2][kStageHalves];
+    __shared__ __attribute__((aligned(16))) uint16_t s_vv[2][kStageHalves];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 31;
+    const int u = lane >> 5;
+
+    const int hg = blockIdx.x;
+    const int half = (a.ntiles + 1) / 2;
+    const int y = (int)blockIdx.y;
+    const int tile = y < half ? a.ntiles - 1 - y : y - half;
+    const int h = hg * HW + (wave % HW);
+    const int kh = (hg * HW) / a.group;
+    const int t0 = tile * TPW;
+    const int tw0 = t0 + 32 * (wave / HW);
+    const int lk = a.pos0 + a.tokens;
+    const int kend_wg = a.pos0 + min(t0 + TPW, a.tokens);
+    const int kend_w = a.pos0 + min(tw0 + 32, a.tokens);
+
+    const int tq = tw0 + col;
+    const bool qvalid = tq < a.tokens;
+    half8 qh[8];
+    u32x4 qraw[16];
+    q_load(a.q + ((size_t)(qvalid ? tq : 0) * a.hq + h) * kDim, u, qraw);
+
+    uint32_t koff[8], voff[4];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) koff[t] = col * 256 + 16 * kswz(col, 2 * t + u);
+    {
+        const int sl = lane & 15, j = sl >> 2;
+        const int low = 2 * ((lane >> 4) & 1) + ((sl & 3) >> 1);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+            voff[dt] = (4 * u + j) * 256 + 16 * (4 * (dt ^ j) + low) + 8 * (sl & 1);
+    }
+    // this lane's rows of the stage (16 wave + lane / 8 + 8 i) and 16-byte code chunk lane % 8
+    const size_t rstride = (size_t)a.hkv * RB;
+    const int rr = lane >> 3, ch = lane & 7;
+    const uint8_t* kbase = a.k + (size_t)kh * RB;
+    const uint8_t* vbase = a.v + (size_t)kh * RB;
+    auto load_rows = [&](int kb, Q8Rows& q) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            // rows past the cache's last valid position are never read: the tile's keys are
+            // below kend_wg <= cap, and rows past lk are finite (masked later)
+            const size_t row = (size_t)(kb + 16 * wave + rr + 8 * i) * rstride;
+            q.kc[i] = *reinterpret_cast<const u32x4*>(kbase + row + 16 * ch);
+            q.vc[i] = *reinterpret_cast<const u32x4*>(vbase + row + 16 * ch);
+            q.ks[i] = *reinterpret_cast<const uint16_t*>(kbase + row + 128 + 2 * (ch >> 1));
+            q.vs[i] = *reinterpret_cast<const uint16_t*>(vbase + row + 128 + 2 * (ch >> 1));
+        }
+    };
+    typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+    // 16 codes -> 16 f16 values code * scale (exact f16 codes, one rounding in the multiply)
+    auto deq = [&](u32x4 c, uint32_t sc, uint32_t (&w)[8]) {
+        const half2 s2 = __builtin_bit_cast(half2, sc | (sc << 16));
+        const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            uint32_t lo, hi;
+            codes4_to_f16(cw[e], lo, hi);
+            w[2 * e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, lo) * s2);
+            w[2 * e + 1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, hi) * s2);
+        }
+    };
+    auto store_rows = [&](const Q8Rows& q, int buf) {
+        uint8_t* kt = reinterpret_cast<uint8_t*>(&s_k[buf][0]);
+        uint8_t* vt = reinterpret_cast<uint8_t*>(&s_vv[buf][0]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int row = 16 * wave + rr + 8 * i;
+            uint32_t w[8];
+            deq(q.kc[i], q.ks[i], w);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                *reinterpret_cast<u32x4*>(kt + row * 256 + 16 * kswz(row, 2 * ch + j)) =
+                    u32x4{w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]};
+            deq(q.vc[i], q.vs[i], w);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                *reinterpret_cast<u32x4*>(vt + row * 256 + 16 * vswz(row, 2 * ch + j)) =
+                    u32x4{w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]};
+        }
+    };
+
+    f32x16 acc[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[dt][i] = 0.0f;
+    float m_used = -INFINITY;
+    float lsum = 0.0f;
+    const int qabs = a.pos0 + tq;
+    const float kGrow = 8.0f / kLog2e;
+
+    auto stage = [&](int kb, int buf) {
+        const uint8_t* kt = reinterpret_cast<const uint8_t*>(&s_k[buf][0]);
+        const uint8_t* vt = reinterpret_cast<const uint8_t*>(&s_vv[buf][0]);
+        const int nsub = (kb + 32 < kend_w) ? 2 : 1;
+        const f32x16 zero = {};
+        f32x16 s[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            if (b < nsub) {
+                s[b] = mfma(lds_b128(reinterpret_cast<const uint16_t*>(kt + koff[0] + b * 32 * 256)), qh[0], zero);
+#pragma unroll
+                for (int t = 1; t < 8; ++t)
+                    s[b] = mfma(lds_b128(reinterpret_cast<const uint16_t*>(kt + koff[t] + b * 32 * 256)), qh[t], s[b]);
+            }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            if (b < nsub) {
+                const int kb2 = kb + 32 * b;
+                if ((kb2 + 31 > a.pos0 + tw0) || (kb2 + 31 >= lk)) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int key = kb2 + 8 * (i / 4) + 4 * u + (i % 4);
+                        s[b][i] = (key > qabs || key >= lk) ? -INFINITY : s[b][i];
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[b][i]);
+            }
+        }
+        tmax = max_xor32(tmax);
+        const bool grow = tmax > m_used + kGrow;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+            const float alpha = grow ? __builtin_amdgcn_exp2f((m_used - tmax) * kLog2e) : 1.0f;
+            if (grow) m_used = tmax;
+            lsum *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
+        }
+        const float mb = m_used * kLog2e;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            if (b >= nsub) break;
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                uint16_t ph[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float p = __builtin_amdgcn_exp2f(fmaf(s[b][8 * st + j], kLog2e, -mb));
+                    lsum += p;
+                    ph[j] = f2h(p);
+                }
+                const half8 pb = pack8(ph);
+                const int rows = (32 * b + 16 * st) * 256;
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) {
+                    const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vt + voff[dt] + rows));
+                    const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vt + voff[dt] + rows + 8 * 256));
+                    const half8 va = __builtin_bit_cast(half8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+                    acc[dt] = mfma(va, pb, acc[dt]);
+                }
+            }
+        }
+    };
+
+    // stage i is converted into buffer i % 2 right after stage i - 1 was contracted (the barrier
+    // before stage i - 1 saw every wave done with stage i - 2, the buffer's previous content);
+    // its raw rows were loaded one stage earlier
+    const int nst = (kend_wg + kTile - 1) / kTile;
+    Q8Rows raw;
+    load_rows(0, raw);
+    q_convert(qraw, a.scale, qvalid, qh);
+    store_rows(raw, 0);
+    if (1 < nst) load_rows(kTile, raw);
+    for (int i = 0; i < nst; ++i) {
+        __syncthreads();  // stage i written by every wave; stage i - 1's buffer free
+        const int kb = i * kTile;
+        if (kb < kend_w) stage(kb, i & 1);
+        if (i + 1 < nst) {
+            store_rows(raw, (i + 1) & 1);
+            if (i + 2 < nst) load_rows((i + 2) * kTile, raw);
+        }
+    }
+
+    const float L = sum_xor32(lsum);
+    const float inv = 1.0f / L;
+    __syncthreads();  // every wave is done with the K stages: wave w stages its output in 8 KB of them
+    store_o_rows(acc, inv, reinterpret_cast<uint8_t*>(&s_k[0][0]) + wave * 32 * 256, lane, a.o, tw0,
+                 a.tokens, a.hq, h);
+}
+
 // Three workgroups per CU: prefill_f16_kernel4's tile code on 32-key stages in a three-stage
 // ring (48 KB of LDS per workgroup), with the per-lane operand offsets recomputed at each use so
 // a wave fits 168 registers and each SIMD holds three waves. The kernel is latency-bound (matrix
@@ -1153,6 +1360,13 @@ int launch_prec(const PrefillArgs& a, int precision, hipStream_t stream) {
     if constexpr (KV == BRASA_KV_F16) {
         if (precision == BRASA_PREFILL_F16) return launch_f16<HW, false>(a, stream);
         if (precision == BRASA_PREFILL_F16_PF32) return launch_f16<HW, true>(a, stream);
+    }
+    if constexpr (KV == BRASA_KV_Q8_0) {
+        if (precision == BRASA_PREFILL_F16) {
+            hipLaunchKernelGGL((prefill_q8_kernel4<HW>), dim3(a.hq / HW, a.ntiles), dim3(kThreads),
+                               0, stream, a);
+            return check_launch("prefill_q8_kernel4");
+        }
     }
     switch (precision) {
         case BRASA_PREFILL_F32: return launch<KV, HW, true, true, true>(a, stream);

@@ -148,3 +148,24 @@ def test_prefill_config_q8_chunk():
                                rows=(tokens - 8, tokens))
     a, r = bars(got[-8:], want[-8:])
     assert a <= 2e-3 and r <= 1e-2
+
+
+@pytest.mark.parametrize("tokens,pos0", [(2048, 0), (512, 16384)])
+def test_prefill_config_q8_every_tile(tokens, pos0):
+    """q8_0 KV cache (quantised from the same post-RMSNorm / RoPE draws), F16 precision: one row
+    of every query tile against the q16 oracle over the dequantised cache."""
+    q, kk, vv = _prefill_inputs(tokens, pos0, 3000 + tokens + pos0)
+    cache = KvPair(KvType.Q8_0, kk, vv)
+    gq = DeviceBuffer.from_array(q)
+    o = DeviceBuffer(tokens * HQ * DIM * 2)
+    _say(f"prefill config q8 T={tokens} pos0={pos0}")
+    Kernels().flash_attention(gq, cache.kbuf, cache.vbuf, o,
+                              AttnShape(tokens, HQ, HKV, DIM, pos0, KvType.Q8_0))
+    synchronize()
+    got = oracle.f16_to_f32(o.download(np.uint16)).reshape(tokens, HQ, DIM)
+    rows = _tile_rows(tokens, 5 + tokens)
+    want, _ = _oracle_rows(q, cache, tokens, pos0, rows)
+    a, r = bars(got[rows], want)
+    print(f"prefill q8 T={tokens} pos0={pos0}, {len(rows)} rows: max-abs {a:.2e} max-rel {r:.2e}")
+    assert a <= 2e-3 and r <= 1e-2
+
