@@ -139,3 +139,25 @@ def test_decode_scratch_too_small():
         k.decode_attention_lanes(q, cache.kbuf, cache.vbuf, part, o,
                                  AttnShape(1, HQ, HKV, DIM, 299, KvType.F16))
     assert e.value.code == 2
+
+
+@pytest.mark.parametrize("vscale", [1e-3, 1e-4, 3e-6])
+def test_decode_q8_small_scales(vscale):
+    """q8_0 caches whose group scales are small or f16-subnormal (|v| ~ vscale): the dequantised
+    products must stay at the reference's bar relative to max|v| (attention.rs:25-32), which
+    rules out rounding p * scale into an f16 subnormal."""
+    k = Kernels()
+    rng = oracle.Rng(57)
+    for pos0 in [300, 4095]:
+        lk = pos0 + 1
+        q = rng.vec(HQ * DIM, 2.0)
+        kv_k = rng.vec(lk * HKV * DIM, 2.0) * np.float32(vscale)
+        kv_v = rng.vec(lk * HKV * DIM, 3.0) * np.float32(vscale)
+        cache = KvPair(KvType.Q8_0, kv_k, kv_v)
+        _say(f"decode q8 small scales {vscale} pos0={pos0}")
+        got = run_decode(k, "lanes", q, cache, HQ, HKV, pos0)
+        want, vmax = oracle.attention(q, cache.k, cache.v, 1, HQ, HKV, DIM, pos0)
+        assert vmax.max() > 0  # scales 1e-4 / 3e-6 groups: f16-subnormal scales, nonzero V
+        w = oracle.worst(got, want, vmax)
+        print(f"q8 scale {vscale} pos0 {pos0}: worst {w:.2e}")
+        assert w <= 1e-5, w
