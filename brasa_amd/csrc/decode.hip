@@ -67,12 +67,15 @@ constexpr int kLongChunk = 512;
 // metadata, so a call allocates and copies nothing).
 constexpr int kMaxSeqs = 64;
 
-// Arrival counters of the in-kernel split merge: kSlotCounters per slot, one per (sequence,
-// head group) of a launch. They start at zero when the library is loaded and every launch
-// returns the counters it uses to zero (the last arrival wraps them), so nothing clears them.
-// Consecutive launches take consecutive slots: launches on different streams only share
+// Arrival counters of the in-kernel split merge: one per (sequence, grid row) of a launch,
+// kCtrStride apart (64 bytes: returning atomics on one line serialize, and with the counters of
+// all rows packed in one line the last arrivals of a 16K-key decode waited ~2 us on each
+// other), kSlotCounters words per slot. They start at zero when the library is loaded and every
+// launch returns the counters it uses to zero (the last arrival wraps them), so nothing clears
+// them. Consecutive launches take consecutive slots: launches on different streams only share
 // counters when kCounterSlots of them are in flight at once.
-constexpr int kSlotCounters = 8192;
+constexpr int kCtrStride = 16;
+constexpr int kSlotCounters = 16384;
 constexpr int kCounterSlots = 64;
 __device__ unsigned g_arrivals[kCounterSlots * kSlotCounters];
 
@@ -114,6 +117,27 @@ __device__ __forceinline__ int seq_of(const DecodeArgs<NS>& a, int col) {
         int si = 0;
         while (si + 1 < a.nseq && col >= a.seq[si + 1].split0) ++si;
         return si;
+    }
+}
+
+// Grid position (row of head groups, split column) of this workgroup for the q8_0 kernel.
+// Workgroup b runs on XCD b % 8 (round-robin dispatch), each XCD with its own L2. A q8_0 row
+// of one KV head is 136 bytes, so adjacent heads share 128-byte lines; with rows varying
+// fastest, the heads of one split sat on eight different XCDs and every shared line was
+// fetched from HBM twice. Here the workgroups b, b + 8, ... (one XCD) take the rows of a
+// column one after another, so the heads of a split share their lines in one L2 (16K keys:
+// 21.5 -> 19.4 us). Any bijection is correct; this one needs the column count to be a
+// multiple of 8 and falls back to rows-fastest otherwise.
+__device__ __forceinline__ void xcd_grid_pos(int rows, int& row, int& col) {
+    const int b = blockIdx.x;
+    const int cols = gridDim.x / rows;
+    if (cols % 8 == 0) {
+        const int j = b >> 3;
+        row = j % rows;
+        col = (j / rows) * 8 + (b & 7);
+    } else {
+        row = b % rows;
+        col = b / rows;
     }
 }
 
@@ -311,7 +335,7 @@ __device__ __forceinline__ void finish_split(const DecodeArgs<NS>& a, const SeqD
     __syncthreads();
     if (threadIdx.x == 0) {
         const int rows = (a.ngroups + HPW - 1) / HPW;
-        unsigned* ctr = a.ctr + si * rows + row;
+        unsigned* ctr = a.ctr + (size_t)(si * rows + row) * kCtrStride;
         const unsigned t = __builtin_amdgcn_atomic_inc32(ctr, (unsigned)(splits - 1),
                                                          __ATOMIC_RELAXED, "agent");
         s_last = t == (unsigned)(splits - 1);
@@ -861,8 +885,8 @@ decode_q8_kernel(DecodeArgs<NS> a) {
     __shared__ __attribute__((aligned(16))) uint8_t s_slot[W][kRing][kQ8Slot];
 
     const int rows = (a.ngroups + HPW - 1) / HPW;
-    const int row = blockIdx.x % rows;
-    const int col = blockIdx.x / rows;
+    int row, col;
+    xcd_grid_pos(rows, row, col);
     const int si = seq_of(a, col);
     const SeqDesc& sd = a.seq[si];
     const int split = col - sd.split0;
@@ -1255,9 +1279,10 @@ int decode_batch_launch(const float* q, const void* const* k, const void* const*
     const int ngroups = per_head ? hq : hkv;
     const size_t oelem = o_f16 ? 2 : 4;
     // sequences per launch: the descriptor array and the counter slot bound it
-    const int per_launch = std::min(kMaxSeqs, std::max(1, kSlotCounters / ngroups));
-    if (ngroups > kSlotCounters)
-        return set_error(BRASA_ERR_SHAPE, "decode: %d head groups exceed %d", ngroups, kSlotCounters);
+    const int per_launch = std::min(kMaxSeqs, std::max(1, kSlotCounters / (kCtrStride * ngroups)));
+    if (ngroups * kCtrStride > kSlotCounters)
+        return set_error(BRASA_ERR_SHAPE, "decode: %d head groups exceed %d", ngroups,
+                         kSlotCounters / kCtrStride);
     size_t part_off = 0;
     for (int b0 = 0; b0 < n; b0 += per_launch) {
         const int nb = std::min(per_launch, n - b0);
