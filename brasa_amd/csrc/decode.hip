@@ -84,6 +84,38 @@ __device__ unsigned g_arrivals[kCounterSlots * kSlotCounters];
 // hq * splits * 130 of them). Every call on a device shares it.
 static __device__ __align__(256) float scratch[BRASA_DECODE_NOALLOC_FLOATS];
 
+#ifdef BRASA_DECODE_TRACE
+// Timeline build (libbrasa_attn_trace.so only): thread 0 of each workgroup writes the 100 MHz
+// real-time counter at the phases of DecodeStamp into slot blockIdx.x % kTraceWgs. The stamps
+// of waves other than wave 0 are not recorded; phases 4 and later wait for every wave.
+constexpr int kTraceWgs = 8192;
+constexpr int kTraceStamps = 16;
+__device__ unsigned long long g_decode_trace[kTraceWgs * kTraceStamps];
+#define DECODE_STAMP(k)                                                                       \
+    do {                                                                                      \
+        if (threadIdx.x == 0)                                                                 \
+            g_decode_trace[(blockIdx.x % kTraceWgs) * kTraceStamps + (k)] =                  \
+                __builtin_amdgcn_s_memrealtime();                                             \
+    } while (0)
+#else
+#define DECODE_STAMP(k) \
+    do {                \
+    } while (0)
+#endif
+// Phases stamped by the timeline build.
+enum DecodeStamp {
+    kStampStart = 0,      // workgroup started
+    kStampFirstBlock,     // wave 0: its first block's loads have landed
+    kStampLastBlock,      // wave 0: its last block's loads have landed
+    kStampWaveDone,       // wave 0: its blocks are computed
+    kStampLdsMerged,      // every wave's state is in LDS
+    kStampStored,         // the workgroup's partials are device-visible
+    kStampArrived,        // the arrival counter returned
+    kStampLoaded,         // last arrival: every split's partial has been loaded
+    kStampMerged,         // last arrival: the splits are merged
+    kStampOut,            // last arrival: o is written
+};
+
 struct SeqDesc {
     const uint8_t* k;     // layer cache base of this sequence
     const uint8_t* v;
@@ -301,6 +333,7 @@ __device__ __forceinline__ void finish_split(const DecodeArgs<NS>& a, const SeqD
         if (u == 0) *reinterpret_cast<f32x2*>(m_ml + (wave * G + c16) * 2) = f32x2{mref, lsum};
     }
     __syncthreads();
+    DECODE_STAMP(kStampLdsMerged);
     const int splits = sd.splits;
     const int q0 = row * HG;
     float* part_acc = a.part + sd.part_off;
@@ -332,6 +365,7 @@ __device__ __forceinline__ void finish_split(const DecodeArgs<NS>& a, const SeqD
     if (splits == 1) return;
     __shared__ int s_last;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores are visible
+    DECODE_STAMP(kStampStored);
     __syncthreads();
     if (threadIdx.x == 0) {
         const int rows = (a.ngroups + HPW - 1) / HPW;
@@ -341,6 +375,7 @@ __device__ __forceinline__ void finish_split(const DecodeArgs<NS>& a, const SeqD
         s_last = t == (unsigned)(splits - 1);
     }
     __syncthreads();
+    DECODE_STAMP(kStampArrived);
     if (!s_last) return;
 
     constexpr int NSG = 64 * W / (HG * 32);  // split groups
@@ -362,6 +397,7 @@ __device__ __forceinline__ void finish_split(const DecodeArgs<NS>& a, const SeqD
             mv[r] = ld_dev8(pm + (size_t)sp * 2);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        DECODE_STAMP(kStampLoaded);
 #pragma unroll
         for (int r = 0; r < kPer; ++r) asm volatile("" : "+v"(av[r]), "+v"(mv[r]));
         // this round's splits: max first, then the weighted sums in split order
@@ -403,7 +439,12 @@ __device__ __forceinline__ void finish_split(const DecodeArgs<NS>& a, const SeqD
             L += w * r_l[t];
         }
     }
+    DECODE_STAMP(kStampMerged);
     if (q0 + cc < a.hq) store_out(a, si, q0 + cc, 4 * q, A / L);
+#ifdef BRASA_DECODE_TRACE
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    DECODE_STAMP(kStampOut);
+#endif
 }
 
 // ---- f32 caches (the reference's exact variant): register-staged K and V -------------------
@@ -654,6 +695,7 @@ __device__ __forceinline__ float sum_rows(float x) {
 template <int G, int NS, int HPW, int W>
 __global__ void __launch_bounds__(64 * W)
 decode_f16_kernel(DecodeArgs<NS> a) {
+    DECODE_STAMP(kStampStart);
     constexpr int RB = 256;
     constexpr int KS = W / HPW;
     static_assert(W <= kMaxLdsWaves, "waves per workgroup");
@@ -762,6 +804,8 @@ decode_f16_kernel(DecodeArgs<NS> a) {
         // block i's 16 instructions were followed by those of the block after it in the ring
         if (i + 1 < nb) wait_k<16>(kr[S]);
         else wait_k<0>(kr[S]);
+        if (i == 0) DECODE_STAMP(kStampFirstBlock);
+        if (i + 1 == nb) DECODE_STAMP(kStampLastBlock);
         const int jb = s0 + kBlock * (ks + KS * i);
         // S^T tiles: rows = keys jb + 16 kt + 4 u + r, column = head (hi / lo half)
         float x[2][4];
@@ -841,6 +885,7 @@ decode_f16_kernel(DecodeArgs<NS> a) {
         __syncthreads();
         fin = reinterpret_cast<float*>(&s_v[0][0][0]);
     }
+    DECODE_STAMP(kStampWaveDone);
     finish_split<G, W, HPW>(a, sd, si, row, split, fin, acc, mref, lsum);
 }
 
@@ -878,6 +923,7 @@ __device__ __forceinline__ void lds_dma4_nt(const uint8_t* src, const void* lds_
 template <int G, int NS, int HPW, int W>
 __global__ void __launch_bounds__(64 * W)
 decode_q8_kernel(DecodeArgs<NS> a) {
+    DECODE_STAMP(kStampStart);
     constexpr int RB = kQ8Row;
     constexpr int KS = W / HPW;
     static_assert(W <= kMaxLdsWaves, "waves per workgroup");
@@ -982,6 +1028,8 @@ decode_q8_kernel(DecodeArgs<NS> a) {
         constexpr int S = decltype(slot_c)::value;
         if (i + 1 < nb) wait_vmcnt<10>();
         else wait_vmcnt<0>();
+        if (i == 0) DECODE_STAMP(kStampFirstBlock);
+        if (i + 1 == nb) DECODE_STAMP(kStampLastBlock);
         const int jb = s0 + kBlock * (ks + KS * i);
         uint8_t* sl = &s_slot[wave][S][0];
         const uint8_t* ksc = sl + 2 * kQ8Codes;
@@ -1131,6 +1179,7 @@ decode_q8_kernel(DecodeArgs<NS> a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[dt][r] += xor_row<G>(acc[dt][r], c16);
     __syncthreads();  // every wave is done with its slots (all copies waited for)
+    DECODE_STAMP(kStampWaveDone);
     finish_split<G, W, HPW>(a, sd, si, row, split, reinterpret_cast<float*>(&s_slot[0][0][0]),
                             acc, mref, lsum);
 }
@@ -1362,3 +1411,13 @@ int decode_launch(const float* q, const void* k, const void* v, float* partials,
 }
 
 }  // namespace brasa
+
+#ifdef BRASA_DECODE_TRACE
+// Copies min(n, kTraceWgs * 16) stamps of the timeline build to host memory `dst`.
+extern "C" int brasa_decode_trace_read(unsigned long long* dst, size_t n) {
+    using namespace brasa;
+    const size_t cnt = std::min(n, (size_t)kTraceWgs * kTraceStamps);
+    const hipError_t e = hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_decode_trace), cnt * sizeof(*dst));
+    return e == hipSuccess ? 0 : BRASA_ERR_LAUNCH;
+}
+#endif

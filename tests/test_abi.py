@@ -14,11 +14,20 @@ from brasa_amd._lib import SYMBOLS, lib
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def _declared():
+TRACE_BLOCK = re.compile(r"#ifdef BRASA_DECODE_TRACE(.*?)#endif", flags=re.S)
+
+
+def _declared(trace=False):
+    """Names the public headers declare: those of the default library, or with trace=True only
+    those of the timeline build (declared under #ifdef BRASA_DECODE_TRACE)."""
     names = set()
     for h in ("brasa_attn.h", "brasa_hip_rt.h"):
         text = open(os.path.join(ROOT, "include", h)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        if trace:
+            text = "\n".join(TRACE_BLOCK.findall(text))
+        else:
+            text = TRACE_BLOCK.sub("", text)
         names |= set(re.findall(r"\b(brasa_\w+)\s*\(", text))
     return names
 
@@ -30,6 +39,18 @@ def test_every_declared_symbol_is_exported_and_bound():
     for name in declared:
         assert hasattr(l, name), name
     assert declared == set(SYMBOLS), declared ^ set(SYMBOLS)
+
+
+def test_timeline_build_exports_the_trace_reader():
+    path = os.path.join(ROOT, "brasa_amd", "libbrasa_attn_trace.so")
+    if not os.path.exists(path):
+        pytest.skip("timeline build not compiled")
+    l = ctypes.CDLL(path)
+    trace = _declared(trace=True)
+    assert trace == {"brasa_decode_trace_read"}
+    for name in trace | _declared():
+        assert hasattr(l, name), name
+    assert not hasattr(ctypes.CDLL(brasa_amd.LIB_PATH), "brasa_decode_trace_read")
 
 
 def test_built_for_gfx950_only():
