@@ -157,9 +157,11 @@ template <> struct Kv8<BRASA_KV_Q8_0> {
 };
 
 // 16-byte HBM -> LDS copy per lane (global_load_lds_dwordx4): lane i writes lds + 16 i.
-// M0 (the LDS base) is saved and restored around it. Issued as inline asm so that the compiler's vector-memory counter bookkeeping never relies on
-// it (its own waits can only become more conservative); the wait before the LDS reads of such
-// a tile is wait_vmcnt below.
+// M0 (the LDS base) is saved and restored around it; an LDS-DMA load needs one wait state after
+// an SALU write of M0 (the s_nop), which the compiler cannot insert inside the asm. Issued as
+// inline asm so that the compiler's vector-memory counter bookkeeping never relies on it (its
+// own waits can only become more conservative); the wait before the LDS reads of such a tile
+// is wait_vmcnt below.
 __device__ __forceinline__ void lds_dma16(const uint8_t* src, uint16_t* lds_wave_base) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)lds_wave_base);
@@ -167,6 +169,7 @@ __device__ __forceinline__ void lds_dma16(const uint8_t* src, uint16_t* lds_wave
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dwordx4 %1, off\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
@@ -181,6 +184,7 @@ __device__ __forceinline__ void lds_dma16_nt(const uint8_t* src, uint16_t* lds_w
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dwordx4 %1, off nt\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
@@ -194,7 +198,36 @@ __device__ __forceinline__ void lds_dma16_s(const uint8_t* sbase, uint32_t voff,
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dwordx4 %1, %2\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(voff), "s"(sbase), "s"(lds_wave_base)
+        : "memory");
+}
+// As lds_dma16_s with the nontemporal hint.
+__device__ __forceinline__ void lds_dma16_s_nt(const uint8_t* sbase, uint32_t voff,
+                                               uint32_t lds_wave_base /* uniform LDS address */) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2 nt\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(voff), "s"(sbase), "s"(lds_wave_base)
+        : "memory");
+}
+// 4-byte variant of lds_dma16_s_nt (lane i writes lds + 4 i).
+__device__ __forceinline__ void lds_dma4_s_nt(const uint8_t* sbase, uint32_t voff,
+                                              uint32_t lds_wave_base /* uniform LDS address */) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dword %1, %2 nt\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
         : "v"(voff), "s"(sbase), "s"(lds_wave_base)

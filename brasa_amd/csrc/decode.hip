@@ -202,6 +202,25 @@ __device__ __forceinline__ void split8(const float (&x)[8], half8& hi, half8& lo
 // (bit for bit what split8 gives). Pairs go through one v_cvt_pk_f16_f32 each and the residual
 // x - hi is one exact fma with the f16 operand (it has at most 13 significant bits), so a lane
 // converts only what its column uses.
+// The hi or the lo part of the products x[j] * f[j] (f16 each), as split8_sel of the rounded
+// products but with lo taken from the exact product: lo = f16(fma(x, f, -hi)). One select on the
+// packed hi halves (zero in hi columns, where the fma then just rounds the product again).
+__device__ __forceinline__ half8 split8_prod_sel(const float (&x)[8], const float (&f)[8],
+                                                 bool lo_part) {
+    typedef _Float16 hf2 __attribute__((ext_vector_type(2)));
+    typedef float ff2 __attribute__((ext_vector_type(2)));
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const ff2 t = {as_f32(x[2 * i] * f[2 * i]), as_f32(x[2 * i + 1] * f[2 * i + 1])};
+        const hf2 h = __builtin_convertvector(t, hf2);
+        const hf2 hs = __builtin_bit_cast(hf2, lo_part ? __builtin_bit_cast(uint32_t, h) : 0u);
+        const ff2 r = {fmaf(x[2 * i], f[2 * i], -(float)hs.x),
+                       fmaf(x[2 * i + 1], f[2 * i + 1], -(float)hs.y)};
+        w[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, hf2));
+    }
+    return as_half8(u32x4{w[0], w[1], w[2], w[3]});
+}
 __device__ __forceinline__ half8 split8_sel(const float (&x)[8], bool lo_part) {
     typedef _Float16 hf2 __attribute__((ext_vector_type(2)));
     typedef float ff2 __attribute__((ext_vector_type(2)));
@@ -907,19 +926,6 @@ constexpr int kQ8Fac = 2 * kQ8Codes + 2 * kBlock * 8;   // K codes, V codes, K s
 constexpr int kQ8Slot = kQ8Fac + kBlock * 4 * 4;         // then V mantissa factors [key][group]
 
 // 4-byte HBM -> LDS copy per lane (global_load_lds_dword, nontemporal): lane i writes lds + 4 i.
-__device__ __forceinline__ void lds_dma4_nt(const uint8_t* src, const void* lds_wave_base) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
-    uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %2\n\t"
-        "global_load_lds_dword %1, off nt\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(src), "s"(m0)
-        : "memory");
-}
-
 template <int G, int NS, int HPW, int W>
 __global__ void __launch_bounds__(64 * W)
 decode_q8_kernel(DecodeArgs<NS> a) {
@@ -938,7 +944,7 @@ decode_q8_kernel(DecodeArgs<NS> a) {
     const int split = col - sd.split0;
     const float* qseq = a.q + (size_t)si * a.hq * kDim;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR math
     const int hl = wave % HPW, ks = wave / HPW;
     const int hg = row * HPW + hl;
     const bool hg_ok = hg < a.ngroups;
@@ -968,26 +974,49 @@ decode_q8_kernel(DecodeArgs<NS> a) {
     }
     // block i -> slot S: K codes (4 instructions, 8 rows each, swizzled), V codes (4, plain),
     // K scales, V scales (one 4-byte instruction each: lane l -> row l / 2, dword l % 2)
+    // Byte offsets of this lane's copies from the block's first row: K code rows 8 r + lane / 8
+    // (16-byte chunk lane % 8, swizzled), V code rows likewise (plain), scale row lane / 2. The
+    // block's base address is uniform (SGPRs), so a full block issues its copies with no address
+    // arithmetic; a block cut by the split's end clamps its rows to the last one.
+    const int lr = lane >> 3, lc = lane & 7, sr = lane >> 1;
+    uint32_t off_k[4], off_v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int rr = 8 * r + lr;
+        off_k[r] = (uint32_t)(rr * kstride) + 16 * (lc ^ ((rr >> 1) & 7));
+        off_v[r] = (uint32_t)(rr * kstride) + 16 * lc;
+    }
+    const uint32_t off_s = (uint32_t)(sr * kstride) + 128 + 4 * (lane & 1);
     auto issue = [&](auto slot_c, int i) {
         constexpr int S = decltype(slot_c)::value;
         const int jb = s0 + kBlock * (ks + KS * i);
-        uint8_t* sl = &s_slot[wave][S][0];
-        const int lr = lane >> 3, lc = lane & 7;
+        const uint32_t sl = lds_addr(&s_slot[wave][S][0]);
+        const uint8_t* kb = kbase + (size_t)jb * kstride;
+        const uint8_t* vb = vbase + (size_t)jb * kstride;
+        if (jb + kBlock <= s1) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int rr = 8 * r + lr;
-            const uint8_t* src = kbase + (size_t)min(jb + rr, s1 - 1) * kstride + 16 * (lc ^ ((rr >> 1) & 7));
-            lds_dma16_nt(src, reinterpret_cast<uint16_t*>(sl + 1024 * r));
-        }
+            for (int r = 0; r < 4; ++r) lds_dma16_s_nt(kb, off_k[r], sl + 1024 * r);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int rr = 8 * r + lr;
-            lds_dma16_nt(vbase + (size_t)min(jb + rr, s1 - 1) * kstride + 16 * lc,
-                         reinterpret_cast<uint16_t*>(sl + kQ8Codes + 1024 * r));
+            for (int r = 0; r < 4; ++r) lds_dma16_s_nt(vb, off_v[r], sl + kQ8Codes + 1024 * r);
+            lds_dma4_s_nt(kb, off_s, sl + 2 * kQ8Codes);
+            lds_dma4_s_nt(vb, off_s, sl + 2 * kQ8Codes + 256);
+        } else {
+            const int last = s1 - 1 - jb;  // rows past it read the last row again
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int rr = 8 * r + lr;
+                const uint32_t row = (uint32_t)(min(rr, last) * kstride);
+                lds_dma16_s_nt(kb, row + 16 * (lc ^ ((rr >> 1) & 7)), sl + 1024 * r);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t row = (uint32_t)(min(8 * r + lr, last) * kstride);
+                lds_dma16_s_nt(vb, row + 16 * lc, sl + kQ8Codes + 1024 * r);
+            }
+            const uint32_t srow = (uint32_t)(min(sr, last) * kstride) + 128 + 4 * (lane & 1);
+            lds_dma4_s_nt(kb, srow, sl + 2 * kQ8Codes);
+            lds_dma4_s_nt(vb, srow, sl + 2 * kQ8Codes + 256);
         }
-        const int sr = lane >> 1;
-        lds_dma4_nt(kbase + (size_t)min(jb + sr, s1 - 1) * kstride + 128 + 4 * (lane & 1), sl + 2 * kQ8Codes);
-        lds_dma4_nt(vbase + (size_t)min(jb + sr, s1 - 1) * kstride + 128 + 4 * (lane & 1), sl + 2 * kQ8Codes + 256);
     };
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
@@ -1145,10 +1174,10 @@ decode_q8_kernel(DecodeArgs<NS> a) {
             }
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                float pg[8];
+                float fg[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) pg[j] = as_f32(p[j] * fk[j][g]);
-                pb[g] = split8_sel(pg, col_lo);
+                for (int j = 0; j < 8; ++j) fg[j] = fk[j][g];
+                pb[g] = split8_prod_sel(p, fg, col_lo);
             }
         }
         const uint16_t* vt = reinterpret_cast<const uint16_t*>(sl);
