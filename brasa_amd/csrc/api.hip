@@ -33,7 +33,7 @@ int decode_batch_launch(const float* q, const void* const* k, const void* const*
                         int hkv, int kv, bool per_head, hipStream_t stream);
 int prefill_launch(const float* q, const void* k, const void* v, void* o, int tokens, int hq,
                    int hkv, int pos0, int kv, int precision, hipStream_t stream);
-void prefill_set_layout(int variant, int pair);
+void prefill_set_layout(int variant, int pair, int parts);
 
 namespace {
 thread_local char g_err[512] = "";
@@ -301,11 +301,13 @@ int brasa_qk_norm_rope_store(int kv, float* q, float* k, const float* v, const f
                                      as_stream(stream));
 }
 
-int brasa_test_set_prefill_layout(int variant, int pair) {
+int brasa_test_set_prefill_layout(int variant, int pair, int parts) {
     g_err[0] = 0;
     if (variant != 0 && variant != 1 && variant != 2 && variant != 4)
         return set_error(BRASA_ERR_ARG, "prefill layout: variant %d (0, 1, 2 or 4)", variant);
-    prefill_set_layout(variant, pair ? 1 : 0);
+    if (parts < 1 || parts > 8)
+        return set_error(BRASA_ERR_ARG, "prefill layout: %d key parts (1 .. 8)", parts);
+    prefill_set_layout(variant, pair ? 1 : 0, parts);
     return BRASA_OK;
 }
 

@@ -233,6 +233,25 @@ __device__ __forceinline__ void lds_dma4_s_nt(const uint8_t* sbase, uint32_t vof
         : "v"(voff), "s"(sbase), "s"(lds_wave_base)
         : "memory");
 }
+// Device-coherent stores and loads (written through / read past the XCD's L2): a partial
+// stored by a workgroup on one XCD is then visible to the merging workgroup on any other.
+__device__ __forceinline__ void st_dev16(float* p, f32x4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void st_dev8(float* p, f32x2 v) {
+    asm volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ f32x4 ld_dev16(const float* p) {
+    f32x4 r;
+    asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(r) : "v"(p) : "memory");
+    return r;
+}
+__device__ __forceinline__ f32x2 ld_dev8(const float* p) {
+    f32x2 r;
+    asm volatile("global_load_dwordx2 %0, %1, off sc1" : "=v"(r) : "v"(p) : "memory");
+    return r;
+}
+
 // LDS address of a __shared__ location, as a 32-bit value.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;

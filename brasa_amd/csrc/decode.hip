@@ -265,25 +265,6 @@ __device__ __forceinline__ int q8_exp(uint16_t sc) {
 }
 
 // ---- the end of a split: merge the W waves, then the splits --------------------------------
-// Device-coherent stores and loads (written through / read past the XCD's L2): a partial
-// stored by a workgroup on one XCD is then visible to the merging workgroup on any other.
-__device__ __forceinline__ void st_dev16(float* p, f32x4 v) {
-    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
-}
-__device__ __forceinline__ void st_dev8(float* p, f32x2 v) {
-    asm volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
-}
-__device__ __forceinline__ f32x4 ld_dev16(const float* p) {
-    f32x4 r;
-    asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(r) : "v"(p) : "memory");
-    return r;
-}
-__device__ __forceinline__ f32x2 ld_dev8(const float* p) {
-    f32x2 r;
-    asm volatile("global_load_dwordx2 %0, %1, off sc1" : "=v"(r) : "v"(p) : "memory");
-    return r;
-}
-
 // (M, A, L) <- merge of (M, A, L) and (m, a, l): M = max, weights 2^(m - M) (0 for an empty side)
 __device__ __forceinline__ void merge_split(float& M, f32x4& A, float& L, float m, f32x4 a,
                                             float l) {

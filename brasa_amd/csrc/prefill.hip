@@ -27,6 +27,7 @@
 //     phases alternate; up to two workgroups per CU), prefill_f16_kernel4 (4 waves, two per CU)
 //     and prefill_f16_kernel4s (4 waves on 32-key stages, three per CU).
 #include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
@@ -53,6 +54,11 @@ struct PrefillArgs {
     int ntiles;                 // query tiles
     int pair;                   // prefill_f16_kernel: workgroup y runs tiles ntiles - 1 - y and y
     float scale;
+    // prefill_f16_kernel key split: each query tile's keys are cut into kparts parts, one
+    // workgroup each; the parts' partials (part) are merged by the last to arrive (ctr)
+    int kparts;
+    float* part;
+    unsigned* ctr;
 };
 
 
@@ -418,12 +424,88 @@ constexpr int kStageHalves = kTile * kDim;  // one 64 x 128 f16 tile
 __device__ __forceinline__ int kswz(int r, int c) { return c ^ (r & 15); }
 __device__ __forceinline__ int vswz(int r, int c) { return c ^ (4 * (r & 3)); }
 
+constexpr bool kKeySplitEnabled = false;
+constexpr int kMaxKeyParts = 8;
+constexpr size_t kKeyPartFloats = 4 * 17 * 64 * 4;  // one part of one query tile
+
+// Key split of prefill_f16_kernel: after its two key groups have merged, each group-0 wave of
+// part `part` holds (acc, m, lsum) of its 32 queries over that part's keys. It stores them to
+// a.part (layout [query tile][part][wave][17 x 16-byte chunks][lane]: acc in 16 chunks, then
+// (m, lsum)) with device-coherent stores, waits until they are visible and counts its arrival
+// on the wave's counter (atomic inc wrapping at kparts - 1, so the last arrival returns it to
+// zero). The last wave to arrive loads every part's state and merges them in part order (max
+// first, then 2^(m_p - max)-weighted sums), so the result does not depend on the arrival
+// order; it returns true and its acc / lsum then hold the merged state. Other waves return false.
+__device__ __forceinline__ bool merge_key_parts(const PrefillArgs& a, int tile, int part, int qw,
+                                             int lane, f32x16 (&acc)[4], float& m_used,
+                                             float& lsum) {
+    constexpr int kChunks = 17;
+    const size_t qt = (size_t)blockIdx.x * a.ntiles + tile;  // query tile (head group, tile)
+    const size_t wave_floats = (size_t)kChunks * 64 * 4;
+    auto state = [&](int p) {
+        return a.part + ((qt * a.kparts + p) * 4 + qw) * wave_floats + 4 * lane;
+    };
+    float* mine = state(part);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            st_dev16(mine + (4 * dt + c) * 256,
+                     f32x4{acc[dt][4 * c], acc[dt][4 * c + 1], acc[dt][4 * c + 2], acc[dt][4 * c + 3]});
+    st_dev16(mine + 16 * 256, f32x4{m_used, lsum, 0.0f, 0.0f});
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's stores are visible
+    unsigned t = 0;
+    if (lane == 0)
+        t = __builtin_amdgcn_atomic_inc32(a.ctr + (qt * 4 + qw) * 16, (unsigned)(a.kparts - 1),
+                                          __ATOMIC_RELAXED, "agent");
+    // (every lane's stores were waited for before lane 0's increment: a wave's instructions
+    // issue in order)
+    if (__builtin_amdgcn_readlane(t, 0) != (unsigned)(a.kparts - 1)) return false;
+
+    // maximum over the parts, then the weighted sums in part order (one 32-dim block at a time)
+    float wp[kMaxKeyParts];
+    float lp[kMaxKeyParts];
+    float M = -INFINITY;
+    for (int p = 0; p < a.kparts; ++p) {
+        const f32x4 ml = p == part ? f32x4{m_used, lsum, 0.0f, 0.0f} : ld_dev16(state(p) + 16 * 256);
+        wp[p] = ml[0];
+        lp[p] = ml[1];
+        M = fmaxf(M, ml[0]);
+    }
+    float L = 0.0f;
+    for (int p = 0; p < a.kparts; ++p) {
+        wp[p] = (wp[p] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((wp[p] - M) * kLog2e);
+        L += wp[p] * lp[p];
+    }
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+        f32x16 sum = {};
+        for (int p = 0; p < a.kparts; ++p) {
+            if (p == part) {
+                sum += wp[p] * acc[dt];
+                continue;
+            }
+            const float* st = state(p) + (4 * dt) * 256;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const f32x4 v = ld_dev16(st + c * 256);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sum[4 * c + j] += wp[p] * v[j];
+            }
+        }
+        acc[dt] = sum;
+    }
+    lsum = L;
+    m_used = M;
+    return true;
+}
+
 // One query tile of prefill_f16_kernel (the workgroup's whole work for it, merge and store
 // included); s_kv = [K / V][group][buffer]: each group streams its own 64-key tiles; K and V
 // have their own double buffers because K of tile i is free after tile i's QK^T, V only after
 // its PV.
 template <int HW, bool PS>
-__device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile,
+__device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile, const int part,
                                             uint16_t (&s_kv)[2][2][2][kStageHalves]) {
     constexpr int TPW = 32 * 4 / HW;
     constexpr int kTileBytes = kStageHalves * 2;
@@ -442,7 +524,10 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
     const int tw0 = t0 + 32 * (qw / HW);
     const int lk = a.pos0 + a.tokens;
     const int kend_wg = a.pos0 + min(t0 + TPW, a.tokens);
-    const int ntile = (kend_wg + kTile - 1) / kTile;   // 64-key tiles the workgroup reads
+    const int ntile_all = (kend_wg + kTile - 1) / kTile;  // 64-key tiles the query tile needs
+    // this workgroup's part of them: tiles [tb, tb + ntile)
+    const int tb = (int)((long long)ntile_all * part / a.kparts);
+    const int ntile = (int)((long long)ntile_all * (part + 1) / a.kparts) - tb;
     const int ng = (ntile - grp + 1) / 2;               // tiles of this wave's group
 
     const int tq = tw0 + col;
@@ -484,7 +569,7 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
     const uint32_t lds_k = lds_addr(&s_kv[0][grp][0][0]) + qw * 16 * 256;
     const uint32_t lds_v = lds_addr(&s_kv[1][grp][0][0]) + qw * 16 * 256;
     // tile i of this group = workgroup tile 2 i + grp, keys [kb(i), kb(i) + 64)
-    auto kb_of = [&](int i) { return (2 * i + grp) * kTile; };
+    auto kb_of = [&](int i) { return (tb + 2 * i + grp) * kTile; };
     // lane-constant copy sources, computed once (8 registers; the copies are issued in the
     // softmax phase, whose VALU slots are the less loaded ones)
     uint32_t kso[4], vso[4];
@@ -711,6 +796,7 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
     }
     __syncthreads();
 
+    if (a.kparts > 1 && !merge_key_parts(a, tile, part, qw, lane, acc, m_used, lsum)) return;
     const float L = sum_xor32(lsum);
     const float inv = 1.0f / L;  // padding columns: never stored
     // this wave's 8 KB of group 0's K buffers: group 0 copies into them only after this
@@ -727,10 +813,15 @@ template <int HW, bool PS>
 __global__ void __launch_bounds__(2 * kThreads, 1)
 prefill_f16_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t s_kv[2][2][2][kStageHalves];
+    if (a.kparts > 1) {  // workgroup y: key part y % kparts of query tile ntiles - 1 - y / kparts
+        f16_pp_tile<HW, PS>(a, a.ntiles - 1 - (int)blockIdx.y / a.kparts,
+                            (int)blockIdx.y % a.kparts, s_kv);
+        return;
+    }
     const int y = blockIdx.y;
     const int heavy = a.ntiles - 1 - y;
-    f16_pp_tile<HW, PS>(a, heavy, s_kv);
-    if (a.pair && y < heavy) f16_pp_tile<HW, PS>(a, y, s_kv);
+    f16_pp_tile<HW, PS>(a, heavy, 0, s_kv);
+    if (a.pair && y < heavy) f16_pp_tile<HW, PS>(a, y, 0, s_kv);
 }
 
 // Four-wave variant (one group, no key split), two workgroups per CU: with many query tiles per
@@ -1331,6 +1422,28 @@ int launch(const PrefillArgs& a, hipStream_t stream) {
 // that cover every kernel at small sizes; the product path never calls it.
 std::atomic<int> g_force_variant{0};  // 0: chosen by size; 1, 2, 4: the kernels above
 std::atomic<int> g_allow_pair{1};
+std::atomic<int> g_force_parts{1};    // key parts of a forced prefill_f16_kernel launch
+
+// Arrival counters of the key-split merge: one per (query tile, wave), 64 bytes apart, in
+// kPfCounterSlots slots taken round robin per launch; zero at load, returned to zero by every
+// launch (the last arrival wraps them).
+constexpr int kPfSlotWords = 16384;
+constexpr int kPfCounterSlots = 64;
+__device__ unsigned g_pf_arrivals[kPfCounterSlots * kPfSlotWords];
+std::atomic<unsigned> g_pf_next_slot{0};
+unsigned* g_pf_ctr_base[64];
+std::once_flag g_pf_ctr_once[64];
+
+// Key parts per query tile for prefill_f16_kernel: 1 (no split) unless the launch has at most
+// half as many workgroups as the 256 CUs and the tiles' keys are long (a short chunk after a
+// long cached prefix, e.g. 512 tokens at pos0 16384: 128 workgroups), then enough parts to
+// give ~256 workgroups of at least 16 64-key tiles each.
+int key_parts(long long wgs, int keys) {
+    if (wgs > 128) return 1;
+    int parts = 1;
+    while (parts < kMaxKeyParts && wgs * parts * 2 <= 256 && keys / (64 * parts * 2) >= 16) parts *= 2;
+    return parts;
+}
 
 template <int HW, bool PS>
 int launch_f16(const PrefillArgs& a, hipStream_t stream) {
@@ -1340,6 +1453,44 @@ int launch_f16(const PrefillArgs& a, hipStream_t stream) {
     if (pick == 1) {
         PrefillArgs b = a;
         b.pair = g_allow_pair.load(std::memory_order_relaxed) && wgs >= 2 * 256;
+        // The key split is switched off (kKeySplitEnabled): its first GPU run gave wrong results
+        // with 2 parts and a memory aperture fault with 3, from a cause not found yet; every
+        // launch takes the unsplit path until it is.
+        int parts = !kKeySplitEnabled ? 1
+                    : variant         ? g_force_parts.load(std::memory_order_relaxed)
+                                      : key_parts(wgs, a.pos0 + a.tokens);
+        if (parts < 1 || parts > kMaxKeyParts || wgs * 4 * 16 > kPfSlotWords) parts = 1;
+        if (parts > 1) {
+            int dev = 0;
+            if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+                return set_error(BRASA_ERR_LAUNCH, "flash_attention: no device");
+            std::call_once(g_pf_ctr_once[dev], [dev] {
+                void* p = nullptr;
+                if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_pf_arrivals)) == hipSuccess)
+                    g_pf_ctr_base[dev] = static_cast<unsigned*>(p);
+            });
+            if (!g_pf_ctr_base[dev])
+                return set_error(BRASA_ERR_LAUNCH, "flash_attention: arrival counters not found");
+            const unsigned slot = g_pf_next_slot.fetch_add(1, std::memory_order_relaxed) % kPfCounterSlots;
+            void* ws = nullptr;
+            const size_t bytes = (size_t)wgs * parts * kKeyPartFloats * sizeof(float);
+            hipError_t e = hipMallocAsync(&ws, bytes, stream);
+            if (e != hipSuccess)
+                return set_error(BRASA_ERR_LAUNCH, "flash_attention: hipMallocAsync(%zu): %s", bytes,
+                                 hipGetErrorString(e));
+            b.pair = 0;
+            b.kparts = parts;
+            b.part = static_cast<float*>(ws);
+            b.ctr = g_pf_ctr_base[dev] + (size_t)slot * kPfSlotWords;
+            hipLaunchKernelGGL((prefill_f16_kernel<HW, PS>), dim3(a.hq / HW, a.ntiles * parts),
+                               dim3(2 * kThreads), 0, stream, b);
+            const int st = check_launch("prefill_f16_kernel");
+            e = hipFreeAsync(ws, stream);
+            if (st != BRASA_OK) return st;
+            if (e != hipSuccess)
+                return set_error(BRASA_ERR_LAUNCH, "flash_attention: hipFreeAsync: %s", hipGetErrorString(e));
+            return BRASA_OK;
+        }
         const int rows = b.pair ? (a.ntiles + 1) / 2 : a.ntiles;
         hipLaunchKernelGGL((prefill_f16_kernel<HW, PS>), dim3(a.hq / HW, rows),
                            dim3(2 * kThreads), 0, stream, b);
@@ -1389,9 +1540,10 @@ int launch_kv(PrefillArgs& a, int precision, hipStream_t stream) {
 
 }  // namespace
 
-void prefill_set_layout(int variant, int pair) {
+void prefill_set_layout(int variant, int pair, int parts) {
     g_force_variant.store(variant, std::memory_order_relaxed);
     g_allow_pair.store(pair, std::memory_order_relaxed);
+    g_force_parts.store(parts, std::memory_order_relaxed);
 }
 
 int prefill_launch(const float* q, const void* k, const void* v, void* o, int tokens, int hq,
@@ -1408,6 +1560,9 @@ int prefill_launch(const float* q, const void* k, const void* v, void* o, int to
     a.pos0 = pos0;
     a.ntiles = 0;
     a.pair = 0;
+    a.kparts = 1;
+    a.part = nullptr;
+    a.ctr = nullptr;
     a.scale = 1.0f / sqrtf(static_cast<float>(kDim));
     switch (kv) {
         case BRASA_KV_F32: return launch_kv<BRASA_KV_F32>(a, precision, stream);

@@ -243,10 +243,12 @@ int brasa_qk_norm_rope_store(int kv, float* q, float* k, const float* v, const f
  * kernel for BRASA_KV_F16 is chosen by workgroup count; tests force each of the three kernels at
  * small sizes with variant 1 (two key groups per workgroup), 2 (four waves) or 4 (four waves,
  * 32-key stages), and 0 restores the choice by size. pair = 0 stops the two-group kernel from
- * pairing heavy and light query tiles (the results are identical either way). Process-wide; set
- * it only while no prefill call is being enqueued on another thread.
+ * pairing heavy and light query tiles (the results are identical either way). parts (1 .. 8)
+ * is the number of workgroups each query tile's keys are split over when variant 1 is forced
+ * (with variant 0 the split is chosen by size: short chunks after long prefixes). Process-wide;
+ * set it only while no prefill call is being enqueued on another thread.
  */
-int brasa_test_set_prefill_layout(int variant, int pair);
+int brasa_test_set_prefill_layout(int variant, int pair, int parts);
 
 #ifdef BRASA_DECODE_TRACE
 /*

@@ -217,3 +217,11 @@ def test_decode_batch_asserts_without_device():
                                                  fake, 32, 8, KvType.F16)) == 5
     # an empty batch is a no-op
     k.decode_attention_batch(fake, [], [], [], Part, fake, 32, 8, KvType.F16)
+
+
+def test_prefill_layout_hook_validates():
+    from brasa_amd._lib import BrasaError, check
+    for bad in [(3, 1, 1), (1, 1, 0), (1, 1, 9)]:
+        with pytest.raises(BrasaError):
+            check(lib().brasa_test_set_prefill_layout(*bad))
+    check(lib().brasa_test_set_prefill_layout(0, 1, 1))

@@ -180,16 +180,16 @@ def test_flash_paired_tiles():
     q = rng.vec(tokens * hq * DIM, 2.0)
     cache = KvPair(KvType.F16, rng.vec(cap * hkv * DIM, 2.0), rng.vec(cap * hkv * DIM, 3.0))
     try:
-        check(lib().brasa_test_set_prefill_layout(1, 1))
+        check(lib().brasa_test_set_prefill_layout(1, 1, 1))
         _say(f"prefill paired F16 hq={hq} T={tokens} pos0={pos0}")
         oh = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
         _say(f"prefill paired F16_PF32 hq={hq} T={tokens} pos0={pos0}")
         op = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16_PF32)
-        check(lib().brasa_test_set_prefill_layout(1, 0))
+        check(lib().brasa_test_set_prefill_layout(1, 0, 1))
         _say(f"prefill unpaired F16 hq={hq} T={tokens} pos0={pos0}")
         ou = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
     finally:
-        check(lib().brasa_test_set_prefill_layout(0, 1))
+        check(lib().brasa_test_set_prefill_layout(0, 1, 1))
     assert np.array_equal(oh, ou)
     for t0, t1 in [(0, 32), (512, 544), (1024, 1040)]:
         ref16, vmax = oracle.attention(q, cache.k, cache.v, tokens, hq, hkv, DIM, pos0,
@@ -200,3 +200,62 @@ def test_flash_paired_tiles():
               f"F16_PF32 worst_f16 {w:.2e}")
         assert a <= 2e-3 and r <= 1e-2, (t0, a, r)
         assert w <= 1e-5, (t0, w)
+
+
+@pytest.mark.skip(reason="prefill key split switched off in the library: its first GPU run gave "
+                  "wrong results (2 parts) and a memory aperture fault (3 parts), cause not found")
+@pytest.mark.parametrize("parts", [2, 3, 8])
+def test_flash_key_split(parts):
+    # A short chunk after a long cached prefix: each query tile's keys split over `parts`
+    # workgroups of the two-group kernel (forced), the parts merged by the last to arrive.
+    # Checked against the oracle on every query row, in both f16 precisions, and against the
+    # unsplit launch (a different merge order: within the bar, not bit-equal).
+    k = Kernels()
+    rng = oracle.Rng(71 + parts)
+    tokens, pos0, hq, hkv = 64, 4000, HQ, HKV
+    lk = pos0 + tokens
+    cap = (lk + 63) // 64 * 64
+    q = rng.vec(tokens * hq * DIM, 2.0)
+    cache = KvPair(KvType.F16, rng.vec(cap * hkv * DIM, 2.0), rng.vec(cap * hkv * DIM, 3.0))
+    try:
+        check(lib().brasa_test_set_prefill_layout(1, 0, parts))
+        _say(f"prefill key split parts={parts} F16 T={tokens} pos0={pos0}")
+        oh = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
+        _say(f"prefill key split parts={parts} F16_PF32 T={tokens} pos0={pos0}")
+        op = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16_PF32)
+        oh2 = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
+        check(lib().brasa_test_set_prefill_layout(1, 0, 1))
+        _say(f"prefill unsplit F16 T={tokens} pos0={pos0}")
+        o1 = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
+    finally:
+        check(lib().brasa_test_set_prefill_layout(0, 1, 1))
+    assert np.array_equal(oh, oh2)  # the merge order is fixed: repeat calls give equal bits
+    ref16, vmax = oracle.attention(q, cache.k, cache.v, tokens, hq, hkv, DIM, pos0, q16=True)
+    a, r = bars(oracle.f16_to_f32(oh), ref16)
+    w = oracle.worst_f16(op, ref16, vmax)
+    a1, r1 = bars(oracle.f16_to_f32(oh), oracle.f16_to_f32(o1))
+    print(f"key split {parts}: F16 max-abs {a:.2e} max-rel {r:.2e}; F16_PF32 worst_f16 {w:.2e}; "
+          f"vs unsplit max-abs {a1:.2e}")
+    assert a <= 2e-3 and r <= 1e-2, (a, r)
+    assert w <= 1e-5, w
+    assert a1 <= 2e-3, a1
+
+
+@pytest.mark.skip(reason="prefill key split switched off in the library: its first GPU run gave "
+                  "wrong results (2 parts) and a memory aperture fault (3 parts), cause not found")
+def test_flash_key_split_chosen_by_size():
+    # 128 query tiles x 8 head groups is below half the CUs: the launch splits the keys by
+    # itself (two parts at 64 tokens after 8192 cached positions)
+    k = Kernels()
+    rng = oracle.Rng(83)
+    tokens, pos0, hq, hkv = 64, 8192, HQ, HKV
+    lk = pos0 + tokens
+    cap = (lk + 63) // 64 * 64
+    q = rng.vec(tokens * hq * DIM, 2.0)
+    cache = KvPair(KvType.F16, rng.vec(cap * hkv * DIM, 2.0), rng.vec(cap * hkv * DIM, 3.0))
+    _say(f"prefill auto split F16 T={tokens} pos0={pos0}")
+    oh = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
+    ref16, vmax = oracle.attention(q, cache.k, cache.v, tokens, hq, hkv, DIM, pos0, q16=True)
+    a, r = bars(oracle.f16_to_f32(oh), ref16)
+    print(f"auto key split: F16 max-abs {a:.2e} max-rel {r:.2e}")
+    assert a <= 2e-3 and r <= 1e-2, (a, r)
