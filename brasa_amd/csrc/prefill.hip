@@ -424,7 +424,7 @@ constexpr int kStageHalves = kTile * kDim;  // one 64 x 128 f16 tile
 __device__ __forceinline__ int kswz(int r, int c) { return c ^ (r & 15); }
 __device__ __forceinline__ int vswz(int r, int c) { return c ^ (4 * (r & 3)); }
 
-constexpr bool kKeySplitEnabled = false;
+constexpr bool kKeySplitEnabled = true;
 constexpr int kMaxKeyParts = 8;
 constexpr size_t kKeyPartFloats = 4 * 17 * 64 * 4;  // one part of one query tile
 
@@ -462,39 +462,56 @@ __device__ __forceinline__ bool merge_key_parts(const PrefillArgs& a, int tile, 
     // issue in order)
     if (__builtin_amdgcn_readlane(t, 0) != (unsigned)(a.kparts - 1)) return false;
 
-    // maximum over the parts, then the weighted sums in part order (one 32-dim block at a time)
-    float wp[kMaxKeyParts];
-    float lp[kMaxKeyParts];
+    // ld_dev16 is a bare load: its registers are written when the data returns, so every batch
+    // of loads below is followed by s_waitcnt vmcnt(0) and an asm that names the loaded
+    // registers, which keeps any use of them (or reuse of those registers) after the wait.
+    // maximum over the parts, then the weighted sums in part order
+    f32x4 ml[kMaxKeyParts];
+#pragma unroll
+    for (int p = 0; p < kMaxKeyParts; ++p)
+        ml[p] = p == part       ? f32x4{m_used, lsum, 0.0f, 0.0f}
+                : p < a.kparts  ? ld_dev16(state(p) + 16 * 256)
+                                : f32x4{-INFINITY, 0.0f, 0.0f, 0.0f};
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int p = 0; p < kMaxKeyParts; ++p) asm volatile("" : "+v"(ml[p]));
     float M = -INFINITY;
-    for (int p = 0; p < a.kparts; ++p) {
-        const f32x4 ml = p == part ? f32x4{m_used, lsum, 0.0f, 0.0f} : ld_dev16(state(p) + 16 * 256);
-        wp[p] = ml[0];
-        lp[p] = ml[1];
-        M = fmaxf(M, ml[0]);
-    }
+#pragma unroll
+    for (int p = 0; p < kMaxKeyParts; ++p)
+        if (p < a.kparts) M = fmaxf(M, ml[p][0]);
+    float wp[kMaxKeyParts];
     float L = 0.0f;
-    for (int p = 0; p < a.kparts; ++p) {
-        wp[p] = (wp[p] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((wp[p] - M) * kLog2e);
-        L += wp[p] * lp[p];
+#pragma unroll
+    for (int p = 0; p < kMaxKeyParts; ++p) {
+        wp[p] = (p >= a.kparts || ml[p][0] == -INFINITY) ? 0.0f
+                                                        : __builtin_amdgcn_exp2f((ml[p][0] - M) * kLog2e);
+        if (p < a.kparts) L += wp[p] * ml[p][1];
     }
+    f32x16 sum[4] = {};
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-        f32x16 sum = {};
-        for (int p = 0; p < a.kparts; ++p) {
-            if (p == part) {
-                sum += wp[p] * acc[dt];
-                continue;
-            }
-            const float* st = state(p) + (4 * dt) * 256;
+    for (int p = 0; p < kMaxKeyParts; ++p) {
+        if (p >= a.kparts) break;
+        if (p == part) {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const f32x4 v = ld_dev16(st + c * 256);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) sum[4 * c + j] += wp[p] * v[j];
-            }
+            for (int dt = 0; dt < 4; ++dt) sum[dt] += wp[p] * acc[dt];
+            continue;
         }
-        acc[dt] = sum;
+        f32x4 v[16];  // part p's accumulator, one round trip
+        const float* st = state(p);
+#pragma unroll
+        for (int c = 0; c < 16; ++c) v[c] = ld_dev16(st + c * 256);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int c = 0; c < 16; ++c) asm volatile("" : "+v"(v[c]));
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sum[dt][4 * c + j] += wp[p] * v[4 * dt + c][j];
     }
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) acc[dt] = sum[dt];
     lsum = L;
     m_used = M;
     return true;
@@ -793,6 +810,7 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
         for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[dt][i] = acc[dt][i] * wa + xch[16 * dt + i] * wb;
+        m_used = M;  // acc and lsum are now relative to M (the key split stores it with them)
     }
     __syncthreads();
 
@@ -1453,9 +1471,6 @@ int launch_f16(const PrefillArgs& a, hipStream_t stream) {
     if (pick == 1) {
         PrefillArgs b = a;
         b.pair = g_allow_pair.load(std::memory_order_relaxed) && wgs >= 2 * 256;
-        // The key split is switched off (kKeySplitEnabled): its first GPU run gave wrong results
-        // with 2 parts and a memory aperture fault with 3, from a cause not found yet; every
-        // launch takes the unsplit path until it is.
         int parts = !kKeySplitEnabled ? 1
                     : variant         ? g_force_parts.load(std::memory_order_relaxed)
                                       : key_parts(wgs, a.pos0 + a.tokens);

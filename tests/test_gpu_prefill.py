@@ -202,8 +202,6 @@ def test_flash_paired_tiles():
         assert w <= 1e-5, (t0, w)
 
 
-@pytest.mark.skip(reason="prefill key split switched off in the library: its first GPU run gave "
-                  "wrong results (2 parts) and a memory aperture fault (3 parts), cause not found")
 @pytest.mark.parametrize("parts", [2, 3, 8])
 def test_flash_key_split(parts):
     # A short chunk after a long cached prefix: each query tile's keys split over `parts`
@@ -241,8 +239,6 @@ def test_flash_key_split(parts):
     assert a1 <= 2e-3, a1
 
 
-@pytest.mark.skip(reason="prefill key split switched off in the library: its first GPU run gave "
-                  "wrong results (2 parts) and a memory aperture fault (3 parts), cause not found")
 def test_flash_key_split_chosen_by_size():
     # 128 query tiles x 8 head groups is below half the CUs: the launch splits the keys by
     # itself (two parts at 64 tokens after 8192 cached positions)
