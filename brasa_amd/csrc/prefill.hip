@@ -424,7 +424,6 @@ constexpr int kStageHalves = kTile * kDim;  // one 64 x 128 f16 tile
 __device__ __forceinline__ int kswz(int r, int c) { return c ^ (r & 15); }
 __device__ __forceinline__ int vswz(int r, int c) { return c ^ (4 * (r & 3)); }
 
-constexpr bool kKeySplitEnabled = true;
 constexpr int kMaxKeyParts = 8;
 constexpr size_t kKeyPartFloats = 4 * 17 * 64 * 4;  // one part of one query tile
 
@@ -1060,7 +1059,8 @@ prefill_q8_kernel4(PrefillArgs a) {
 
     const int hg = blockIdx.x;
     const int half = (a.ntiles + 1) / 2;
-    const int y = (int)blockIdx.y;
+    const int y = (int)blockIdx.y / a.kparts;  // query tile order; key part y % kparts
+    const int part = (int)blockIdx.y % a.kparts;
     const int tile = y < half ? a.ntiles - 1 - y : y - half;
     const int h = hg * HW + (wave % HW);
     const int kh = (hg * HW) / a.group;
@@ -1217,25 +1217,29 @@ prefill_q8_kernel4(PrefillArgs a) {
     // stage i is converted into buffer i % 2 right after stage i - 1 was contracted (the barrier
     // before stage i - 1 saw every wave done with stage i - 2, the buffer's previous content);
     // its raw rows were loaded one stage earlier
-    const int nst = (kend_wg + kTile - 1) / kTile;
+    // this workgroup's key stages: [sb, sb + nst) of the tile's (all of them without a key split)
+    const int nst_all = (kend_wg + kTile - 1) / kTile;
+    const int sb = (int)((long long)nst_all * part / a.kparts);
+    const int nst = (int)((long long)nst_all * (part + 1) / a.kparts) - sb;
     Q8Rows raw;
-    load_rows(0, raw);
+    load_rows(sb * kTile, raw);
     q_convert(qraw, a.scale, qvalid, qh);
     store_rows(raw, 0);
-    if (1 < nst) load_rows(kTile, raw);
+    if (1 < nst) load_rows((sb + 1) * kTile, raw);
     for (int i = 0; i < nst; ++i) {
         __syncthreads();  // stage i written by every wave; stage i - 1's buffer free
-        const int kb = i * kTile;
+        const int kb = (sb + i) * kTile;
         if (kb < kend_w) stage(kb, i & 1);
         if (i + 1 < nst) {
             store_rows(raw, (i + 1) & 1);
-            if (i + 2 < nst) load_rows((i + 2) * kTile, raw);
+            if (i + 2 < nst) load_rows((sb + i + 2) * kTile, raw);
         }
     }
 
+    __syncthreads();  // every wave is done with the K stages: wave w stages its output in 8 KB of them
+    if (a.kparts > 1 && !merge_key_parts(a, tile, part, wave, lane, acc, m_used, lsum)) return;
     const float L = sum_xor32(lsum);
     const float inv = 1.0f / L;
-    __syncthreads();  // every wave is done with the K stages: wave w stages its output in 8 KB of them
     store_o_rows(acc, inv, reinterpret_cast<uint8_t*>(&s_k[0][0]) + wave * 32 * 256, lane, a.o, tw0,
                  a.tokens, a.hq, h);
 }
@@ -1452,15 +1456,55 @@ std::atomic<unsigned> g_pf_next_slot{0};
 unsigned* g_pf_ctr_base[64];
 std::once_flag g_pf_ctr_once[64];
 
-// Key parts per query tile for prefill_f16_kernel: 1 (no split) unless the launch has at most
-// half as many workgroups as the 256 CUs and the tiles' keys are long (a short chunk after a
-// long cached prefix, e.g. 512 tokens at pos0 16384: 128 workgroups), then enough parts to
-// give ~256 workgroups of at least 16 64-key tiles each.
-int key_parts(long long wgs, int keys) {
-    if (wgs > 128) return 1;
+// Key parts per query tile: 1 (no split) unless the launch fills at most half of the
+// workgroup slots (`slots`: CUs x workgroups per CU of the kernel) and the tiles' keys are long
+// (a short chunk after a long cached prefix, e.g. 512 tokens at pos0 16384: 128 workgroups),
+// then enough parts to fill the slots with parts of at least 16 64-key tiles each.
+int key_parts(long long wgs, int keys, int slots) {
     int parts = 1;
-    while (parts < kMaxKeyParts && wgs * parts * 2 <= 256 && keys / (64 * parts * 2) >= 16) parts *= 2;
+    while (parts < kMaxKeyParts && wgs * parts * 2 <= slots && keys / (64 * parts * 2) >= 16) parts *= 2;
     return parts;
+}
+
+// Launches `kernel` over (hq / HW) x (rows * parts) workgroups with a key split of `parts`:
+// the arrival counters of the launch (a slot of g_pf_arrivals) and a stream-ordered workspace
+// for the parts' partials, freed on the same stream after the kernel.
+template <typename K>
+int launch_split(K kernel, const char* name, PrefillArgs b, int hw, long long wgs, int parts,
+                 int threads, hipStream_t stream) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return set_error(BRASA_ERR_LAUNCH, "flash_attention: no device");
+    std::call_once(g_pf_ctr_once[dev], [dev] {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_pf_arrivals)) == hipSuccess)
+            g_pf_ctr_base[dev] = static_cast<unsigned*>(p);
+    });
+    if (!g_pf_ctr_base[dev])
+        return set_error(BRASA_ERR_LAUNCH, "flash_attention: arrival counters not found");
+    const unsigned slot = g_pf_next_slot.fetch_add(1, std::memory_order_relaxed) % kPfCounterSlots;
+    void* ws = nullptr;
+    const size_t bytes = (size_t)wgs * parts * kKeyPartFloats * sizeof(float);
+    hipError_t e = hipMallocAsync(&ws, bytes, stream);
+    if (e != hipSuccess)
+        return set_error(BRASA_ERR_LAUNCH, "flash_attention: hipMallocAsync(%zu): %s", bytes,
+                         hipGetErrorString(e));
+    b.pair = 0;
+    b.kparts = parts;
+    b.part = static_cast<float*>(ws);
+    b.ctr = g_pf_ctr_base[dev] + (size_t)slot * kPfSlotWords;
+    hipLaunchKernelGGL(kernel, dim3(b.hq / hw, b.ntiles * parts), dim3(threads), 0, stream, b);
+    const int st = check_launch(name);
+    e = hipFreeAsync(ws, stream);
+    if (st != BRASA_OK) return st;
+    if (e != hipSuccess)
+        return set_error(BRASA_ERR_LAUNCH, "flash_attention: hipFreeAsync: %s", hipGetErrorString(e));
+    return BRASA_OK;
+}
+
+// parts within the limits of the workspace layout and the counter slot, else 1
+int clamp_parts(int parts, long long wgs) {
+    return (parts < 1 || parts > kMaxKeyParts || wgs * 4 * 16 > kPfSlotWords) ? 1 : parts;
 }
 
 template <int HW, bool PS>
@@ -1471,41 +1515,12 @@ int launch_f16(const PrefillArgs& a, hipStream_t stream) {
     if (pick == 1) {
         PrefillArgs b = a;
         b.pair = g_allow_pair.load(std::memory_order_relaxed) && wgs >= 2 * 256;
-        int parts = !kKeySplitEnabled ? 1
-                    : variant         ? g_force_parts.load(std::memory_order_relaxed)
-                                      : key_parts(wgs, a.pos0 + a.tokens);
-        if (parts < 1 || parts > kMaxKeyParts || wgs * 4 * 16 > kPfSlotWords) parts = 1;
-        if (parts > 1) {
-            int dev = 0;
-            if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
-                return set_error(BRASA_ERR_LAUNCH, "flash_attention: no device");
-            std::call_once(g_pf_ctr_once[dev], [dev] {
-                void* p = nullptr;
-                if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_pf_arrivals)) == hipSuccess)
-                    g_pf_ctr_base[dev] = static_cast<unsigned*>(p);
-            });
-            if (!g_pf_ctr_base[dev])
-                return set_error(BRASA_ERR_LAUNCH, "flash_attention: arrival counters not found");
-            const unsigned slot = g_pf_next_slot.fetch_add(1, std::memory_order_relaxed) % kPfCounterSlots;
-            void* ws = nullptr;
-            const size_t bytes = (size_t)wgs * parts * kKeyPartFloats * sizeof(float);
-            hipError_t e = hipMallocAsync(&ws, bytes, stream);
-            if (e != hipSuccess)
-                return set_error(BRASA_ERR_LAUNCH, "flash_attention: hipMallocAsync(%zu): %s", bytes,
-                                 hipGetErrorString(e));
-            b.pair = 0;
-            b.kparts = parts;
-            b.part = static_cast<float*>(ws);
-            b.ctr = g_pf_ctr_base[dev] + (size_t)slot * kPfSlotWords;
-            hipLaunchKernelGGL((prefill_f16_kernel<HW, PS>), dim3(a.hq / HW, a.ntiles * parts),
-                               dim3(2 * kThreads), 0, stream, b);
-            const int st = check_launch("prefill_f16_kernel");
-            e = hipFreeAsync(ws, stream);
-            if (st != BRASA_OK) return st;
-            if (e != hipSuccess)
-                return set_error(BRASA_ERR_LAUNCH, "flash_attention: hipFreeAsync: %s", hipGetErrorString(e));
-            return BRASA_OK;
-        }
+        // one workgroup per CU
+        const int parts = clamp_parts(variant ? g_force_parts.load(std::memory_order_relaxed)
+                                              : key_parts(wgs, a.pos0 + a.tokens, 256), wgs);
+        if (parts > 1)
+            return launch_split(prefill_f16_kernel<HW, PS>, "prefill_f16_kernel", b, HW, wgs, parts,
+                                2 * kThreads, stream);
         const int rows = b.pair ? (a.ntiles + 1) / 2 : a.ntiles;
         hipLaunchKernelGGL((prefill_f16_kernel<HW, PS>), dim3(a.hq / HW, rows),
                            dim3(2 * kThreads), 0, stream, b);
@@ -1529,6 +1544,12 @@ int launch_prec(const PrefillArgs& a, int precision, hipStream_t stream) {
     }
     if constexpr (KV == BRASA_KV_Q8_0) {
         if (precision == BRASA_PREFILL_F16) {
+            // two workgroups per CU
+            const long long wgs = (long long)(a.hq / HW) * a.ntiles;
+            const int parts = clamp_parts(key_parts(wgs, a.pos0 + a.tokens, 512), wgs);
+            if (parts > 1)
+                return launch_split(prefill_q8_kernel4<HW>, "prefill_q8_kernel4", a, HW, wgs, parts,
+                                    kThreads, stream);
             hipLaunchKernelGGL((prefill_q8_kernel4<HW>), dim3(a.hq / HW, a.ntiles), dim3(kThreads),
                                0, stream, a);
             return check_launch("prefill_q8_kernel4");

@@ -239,6 +239,26 @@ def test_flash_key_split(parts):
     assert a1 <= 2e-3, a1
 
 
+def test_flash_key_split_q8():
+    # q8_0 cache, F16 precision: 64 tokens after 8192 cached positions is 16 workgroups of the
+    # q8_0 kernel, which the launch splits into 8 key parts by itself
+    k = Kernels()
+    rng = oracle.Rng(89)
+    tokens, pos0, hq, hkv = 64, 8192, HQ, HKV
+    lk = pos0 + tokens
+    cap = (lk + 63) // 64 * 64
+    q = rng.vec(tokens * hq * DIM, 2.0)
+    cache = KvPair(KvType.Q8_0, rng.vec(cap * hkv * DIM, 2.0), rng.vec(cap * hkv * DIM, 3.0))
+    _say(f"prefill q8_0 auto split F16 T={tokens} pos0={pos0}")
+    oh = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
+    oh2 = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
+    assert np.array_equal(oh, oh2)
+    ref16, vmax = oracle.attention(q, cache.k, cache.v, tokens, hq, hkv, DIM, pos0, q16=True)
+    a, r = bars(oracle.f16_to_f32(oh), ref16)
+    print(f"q8_0 key split: F16 max-abs {a:.2e} max-rel {r:.2e}")
+    assert a <= 2e-3 and r <= 1e-2, (a, r)
+
+
 def test_flash_key_split_chosen_by_size():
     # 128 query tiles x 8 head groups is below half the CUs: the launch splits the keys by
     # itself (two parts at 64 tokens after 8192 cached positions)
