@@ -11,8 +11,11 @@
  *     (crates/metal/src/runtime.rs:255-295), is passed as the already-offset pointer.
  *   - `stream` is a hipStream_t passed as void* (NULL = the default stream). Work is enqueued,
  *     never waited for; ordering is the stream's, as the reference's one in-order command queue.
- *   - No entry point allocates device memory or keeps mutable global state (the kernel table is
- *     static). Scratch (`partials`) is caller-owned, sized by brasa_decode_partials_len().
+ *   - Decode scratch (`partials`) is caller-owned, sized by brasa_decode_partials_len(). The
+ *     library's own device state is its arrival counters (the in-kernel split merges of decode
+ *     and of prefill's key split; each launch returns the ones it uses to zero) and the
+ *     no-allocation entry point's array. The one allocation inside an entry point is prefill's
+ *     key-split workspace (see brasa_flash_attention_with).
  *   - Return value: BRASA_OK (0) or a BRASA_ERR_* code; brasa_last_error() then describes it
  *     (thread-local string, valid until the next call on the same thread).
  *
@@ -182,7 +185,12 @@ int brasa_decode_attention_batch(const float* q, const void* const* k, const voi
  * BRASA_PREFILL_F16 / BRASA_PREFILL_F16_PF32 (Q*scale rounded to f16 as the reference does,
  * fp32 softmax and accumulation) or f32 for BRASA_PREFILL_F32. Requires dim == 128 and
  * hq % hkv == 0; when hq / hkv is not in {1, 2, 4, 8} only BRASA_PREFILL_F32 is accepted
- * (BRASA_ERR_UNSUPPORTED otherwise), as the reference asserts (lib.rs:1227-1231).
+ * (BRASA_ERR_UNSUPPORTED otherwise), as the reference asserts (lib.rs:1227-1231). A launch
+ * that would fill at most half of the GPU with long key ranges per query tile (a short chunk
+ * after a long cached prefix, e.g. 512 tokens at pos0 16384) splits each tile's keys over up to
+ * 8 workgroups; their partials go to a workspace taken with hipMallocAsync and released with
+ * hipFreeAsync on `stream` (68 KB per part and query tile). The result does not depend on the
+ * order in which the parts finish.
  */
 int brasa_flash_attention_with(const float* q, const void* k, const void* v, void* o,
                                brasa_attn_shape shape, int precision, void* stream);
