@@ -191,6 +191,14 @@ __device__ __forceinline__ void lds_dma16_nt(const uint8_t* src, uint16_t* lds_w
         : "v"(src), "s"(m0)
         : "memory");
 }
+// A uniform 64-bit address as the SGPR pair an `s` asm operand needs (readfirstlane of both
+// halves: free when the compiler already holds it in SGPRs).
+__device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
+}
 // As lds_dma16 with a uniform 64-bit base in SGPRs and a per-lane 32-bit byte offset.
 __device__ __forceinline__ void lds_dma16_s(const uint8_t* sbase, uint32_t voff,
                                             uint32_t lds_wave_base /* uniform LDS address */) {
@@ -202,7 +210,7 @@ __device__ __forceinline__ void lds_dma16_s(const uint8_t* sbase, uint32_t voff,
         "global_load_lds_dwordx4 %1, %2\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
-        : "v"(voff), "s"(sbase), "s"(lds_wave_base)
+        : "v"(voff), "s"(uniform_ptr(sbase)), "s"(lds_wave_base)
         : "memory");
 }
 // As lds_dma16_s with the nontemporal hint.
@@ -216,7 +224,7 @@ __device__ __forceinline__ void lds_dma16_s_nt(const uint8_t* sbase, uint32_t vo
         "global_load_lds_dwordx4 %1, %2 nt\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
-        : "v"(voff), "s"(sbase), "s"(lds_wave_base)
+        : "v"(voff), "s"(uniform_ptr(sbase)), "s"(lds_wave_base)
         : "memory");
 }
 // 4-byte variant of lds_dma16_s_nt (lane i writes lds + 4 i).
@@ -230,7 +238,7 @@ __device__ __forceinline__ void lds_dma4_s_nt(const uint8_t* sbase, uint32_t vof
         "global_load_lds_dword %1, %2 nt\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
-        : "v"(voff), "s"(sbase), "s"(lds_wave_base)
+        : "v"(voff), "s"(uniform_ptr(sbase)), "s"(lds_wave_base)
         : "memory");
 }
 // Device-coherent stores and loads (written through / read past the XCD's L2): a partial

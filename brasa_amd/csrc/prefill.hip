@@ -62,6 +62,43 @@ struct PrefillArgs {
 };
 
 
+#ifdef BRASA_PREFILL_TRACE
+// Timeline build (libbrasa_attn_trace.so only): thread 0 of each prefill_f16_kernel workgroup
+// (wave 0: group 0, first head) writes the 100 MHz real-time counter at the phases of
+// PrefillStamp into slot (blockIdx.x + gridDim.x * blockIdx.y) % kPfTraceWgs.
+constexpr int kPfTraceWgs = 8192;
+constexpr int kPfTraceStamps = 16;
+__device__ unsigned long long g_prefill_trace[kPfTraceWgs * kPfTraceStamps];
+#define PREFILL_STAMP(k)                                                                        \
+    do {                                                                                        \
+        if (threadIdx.x == 0)                                                                   \
+            g_prefill_trace[((blockIdx.x + gridDim.x * blockIdx.y) % kPfTraceWgs) *           \
+                                kPfTraceStamps + (k)] = __builtin_amdgcn_s_memrealtime();      \
+    } while (0)
+#else
+#define PREFILL_STAMP(k) \
+    do {                 \
+    } while (0)
+#endif
+// Phases of each query tile a workgroup runs (ti = 0 for its first tile, 1 for the second),
+// stamped at 1 + 6 ti + phase; stamp 0 is the workgroup's start.
+enum PrefillStamp {
+    kPfTileStart = 0,   // the tile's code entered
+    kPfPrologue,        // Q loaded, converted and exchanged; the first copies issued
+    kPfFirstTile,       // the first K/V tile landed (wave 0's first wait and barrier)
+    kPfLoopEnd,         // every key tile contracted
+    kPfMerged,          // the two key groups merged
+    kPfStored,          // o written (the timeline build waits for the stores)
+};
+
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS operations, not for its
+// outstanding global loads (which __syncthreads' fence also waits for).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // x is materialised as one f32 value for both halves (see as_f32): a product folded into a
 // single-rounding conversion for hi alone would leave hi + lo one f16 ulp off at f16 ties.
 __device__ __forceinline__ void split_f16(float x, uint16_t& hi, uint16_t& lo) {
@@ -520,9 +557,15 @@ __device__ __forceinline__ bool merge_key_parts(const PrefillArgs& a, int tile, 
 // included); s_kv = [K / V][group][buffer]: each group streams its own 64-key tiles; K and V
 // have their own double buffers because K of tile i is free after tile i's QK^T, V only after
 // its PV.
+// qraw: this wave's raw half Q row. With q_ready it already holds the tile's Q, loaded by the
+// previous tile's call (next_tile) while that tile merged and stored; next_tile >= 0 loads the
+// next tile's Q into it the same way.
 template <int HW, bool PS>
 __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile, const int part,
-                                            uint16_t (&s_kv)[2][2][2][kStageHalves]) {
+                                            const int ti, uint16_t (&s_kv)[2][2][2][kStageHalves],
+                                            u32x4 (&qraw)[8], const bool q_ready,
+                                            const int next_tile) {
+    PREFILL_STAMP(1 + 6 * ti + kPfTileStart);
     constexpr int TPW = 32 * 4 / HW;
     constexpr int kTileBytes = kStageHalves * 2;
 
@@ -549,8 +592,14 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
     const int tq = tw0 + col;
     const bool qvalid = tq < a.tokens;
     half8 qh[8];
-    u32x4 qraw[8];
-    q_load_half(a.q + ((size_t)(qvalid ? tq : 0) * a.hq + h) * kDim, u, grp, qraw);
+    if (q_ready) {
+        // the loads were issued before the previous tile's output stores: this waits for them
+        // only (the stores may still be in flight), before this tile's copies are issued
+#pragma unroll
+        for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(qraw[j]));
+    } else {
+        q_load_half(a.q + ((size_t)(qvalid ? tq : 0) * a.hq + h) * kDim, u, grp, qraw);
+    }
 
     // lane-constant byte offsets: K operand rows (per k-step t), V^T tr16 sources (per dt),
     // DMA sources (per row quad r)
@@ -760,6 +809,7 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
             qh[t] = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(
                 reinterpret_cast<const uint8_t*>(&s_kv[1][t >> 2][1][0]) + ((qw * 4 + (t & 3)) * 64 + lane) * 16));
     }
+    PREFILL_STAMP(1 + 6 * ti + kPfPrologue);
     // Both groups run the same loop (MFMA phase k, barrier, softmax phase k, barrier); group 1
     // passes one extra barrier before it and group 0 one after it, so the barrier counts match
     // while group 1 runs one phase behind: each group's MFMA phase overlaps the other group's
@@ -770,6 +820,7 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
         const bool on = k <= ng;
         if (on) wait_for(k);
         __syncthreads();
+        if (k == 0) PREFILL_STAMP(1 + 6 * ti + kPfFirstTile);
         if (on) mphase(k);
         __syncthreads();
         // after the barrier every wave of the group has read K(k) and V(k - 1): their buffers
@@ -779,9 +830,19 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
     }
     if (grp == 0) __syncthreads();
     wait_vmcnt<0>();
+    PREFILL_STAMP(1 + 6 * ti + kPfLoopEnd);
 
     // ---- merge the two groups' key halves: group 1 hands (m, l, O) to group 0 through LDS ---
     __syncthreads();  // all tiles contracted, every copy waited for
+    // The next tile's Q is loaded once this tile's LDS exchange is done (issued earlier, the
+    // eight waves' loads delay the exchange behind them on the CU's vector-memory issue), in
+    // flight during this tile's output stores. The barriers below order LDS accesses only.
+    auto prefetch_q = [&]() {
+        if (next_tile >= 0) {
+            const int ntq = next_tile * TPW + 32 * (qw / HW) + col;
+            q_load_half(a.q + ((size_t)(ntq < a.tokens ? ntq : 0) * a.hq + h) * kDim, u, grp, qraw);
+        }
+    };
     float* xch = reinterpret_cast<float*>(&s_kv[0][0][0][0]) + (size_t)(qw * 64 + lane) * 67;
     if (grp == 1) {
 #pragma unroll
@@ -791,11 +852,12 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
         xch[64] = m_used;
         xch[65] = lsum;
     }
-    __syncthreads();
+    lds_barrier();
     // the last barrier of the tile: after it the exchange area (the LDS of the next tile's
     // copies) has been read
     if (grp == 1) {
-        __syncthreads();
+        lds_barrier();
+        prefetch_q();
         return;
     }
     {
@@ -811,7 +873,9 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
             for (int i = 0; i < 16; ++i) acc[dt][i] = acc[dt][i] * wa + xch[16 * dt + i] * wb;
         m_used = M;  // acc and lsum are now relative to M (the key split stores it with them)
     }
-    __syncthreads();
+    lds_barrier();
+    PREFILL_STAMP(1 + 6 * ti + kPfMerged);
+    prefetch_q();
 
     if (a.kparts > 1 && !merge_key_parts(a, tile, part, qw, lane, acc, m_used, lsum)) return;
     const float L = sum_xor32(lsum);
@@ -820,6 +884,10 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
     // epilogue; group 1, possibly in its next tile already, uses its own buffers
     store_o_rows(acc, inv, reinterpret_cast<uint8_t*>(&s_kv[0][0][0][0]) + qw * 32 * 256, lane, a.o,
                  tw0, a.tokens, a.hq, h);
+#ifdef BRASA_PREFILL_TRACE
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    PREFILL_STAMP(1 + 6 * ti + kPfStored);
+#endif
 }
 
 // Work order: head groups fastest (they spread over the XCDs), query tiles heaviest first. With
@@ -830,15 +898,18 @@ template <int HW, bool PS>
 __global__ void __launch_bounds__(2 * kThreads, 1)
 prefill_f16_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t s_kv[2][2][2][kStageHalves];
+    PREFILL_STAMP(0);
+    u32x4 qraw[8];
     if (a.kparts > 1) {  // workgroup y: key part y % kparts of query tile ntiles - 1 - y / kparts
         f16_pp_tile<HW, PS>(a, a.ntiles - 1 - (int)blockIdx.y / a.kparts,
-                            (int)blockIdx.y % a.kparts, s_kv);
+                            (int)blockIdx.y % a.kparts, 0, s_kv, qraw, false, -1);
         return;
     }
     const int y = blockIdx.y;
     const int heavy = a.ntiles - 1 - y;
-    f16_pp_tile<HW, PS>(a, heavy, 0, s_kv);
-    if (a.pair && y < heavy) f16_pp_tile<HW, PS>(a, y, 0, s_kv);
+    const bool second = a.pair && y < heavy;
+    f16_pp_tile<HW, PS>(a, heavy, 0, 0, s_kv, qraw, false, second ? y : -1);
+    if (second) f16_pp_tile<HW, PS>(a, y, 0, 1, s_kv, qraw, true, -1);
 }
 
 // Four-wave variant (one group, no key split), two workgroups per CU: with many query tiles per
@@ -1609,3 +1680,13 @@ int prefill_launch(const float* q, const void* k, const void* v, void* o, int to
 }
 
 }  // namespace brasa
+
+#ifdef BRASA_PREFILL_TRACE
+// Copies min(n, 8192 * 16) stamps of the timeline build to host memory `dst`.
+extern "C" int brasa_prefill_trace_read(unsigned long long* dst, size_t n) {
+    using namespace brasa;
+    const size_t cnt = std::min(n, (size_t)kPfTraceWgs * kPfTraceStamps);
+    const hipError_t e = hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_prefill_trace), cnt * sizeof(*dst));
+    return e == hipSuccess ? 0 : BRASA_ERR_LAUNCH;
+}
+#endif

@@ -258,13 +258,15 @@ int brasa_qk_norm_rope_store(int kv, float* q, float* k, const float* v, const f
  */
 int brasa_test_set_prefill_layout(int variant, int pair, int parts);
 
-#ifdef BRASA_DECODE_TRACE
+#ifdef BRASA_TIMELINE_BUILD
 /*
- * Timeline build only (libbrasa_attn_trace.so; no counterpart in the reference): copies up to n
- * of the decode kernels' phase stamps (16 per workgroup slot, 100 MHz real-time counter, slot =
- * workgroup index mod 8192) to host memory. Read by brasa_amd/decode_timeline.py.
+ * Timeline build only (libbrasa_attn_trace.so; no counterpart in the reference): copy up to n
+ * of the decode / prefill_f16_kernel phase stamps (16 per workgroup slot, 100 MHz real-time
+ * counter, slot = linear workgroup index mod 8192) to host memory. Read by
+ * brasa_amd/decode_timeline.py and brasa_amd/prefill_timeline.py.
  */
 int brasa_decode_trace_read(unsigned long long* dst, size_t n);
+int brasa_prefill_trace_read(unsigned long long* dst, size_t n);
 #endif
 
 /* Description of the last error on this thread ("" if none). */

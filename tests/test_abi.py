@@ -14,12 +14,12 @@ from brasa_amd._lib import SYMBOLS, lib
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-TRACE_BLOCK = re.compile(r"#ifdef BRASA_DECODE_TRACE(.*?)#endif", flags=re.S)
+TRACE_BLOCK = re.compile(r"#ifdef BRASA_TIMELINE_BUILD(.*?)#endif", flags=re.S)
 
 
 def _declared(trace=False):
     """Names the public headers declare: those of the default library, or with trace=True only
-    those of the timeline build (declared under #ifdef BRASA_DECODE_TRACE)."""
+    those of the timeline build (declared under #ifdef BRASA_TIMELINE_BUILD)."""
     names = set()
     for h in ("brasa_attn.h", "brasa_hip_rt.h"):
         text = open(os.path.join(ROOT, "include", h)).read()
@@ -47,10 +47,11 @@ def test_timeline_build_exports_the_trace_reader():
         pytest.skip("timeline build not compiled")
     l = ctypes.CDLL(path)
     trace = _declared(trace=True)
-    assert trace == {"brasa_decode_trace_read"}
+    assert trace == {"brasa_decode_trace_read", "brasa_prefill_trace_read"}
     for name in trace | _declared():
         assert hasattr(l, name), name
-    assert not hasattr(ctypes.CDLL(brasa_amd.LIB_PATH), "brasa_decode_trace_read")
+    for name in trace:
+        assert not hasattr(ctypes.CDLL(brasa_amd.LIB_PATH), name), name
 
 
 def test_built_for_gfx950_only():
