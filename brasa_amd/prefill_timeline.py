@@ -81,6 +81,9 @@ def run(tokens: int, pos0: int, reps: int = 5) -> dict:
     table.free()
     t = t.reshape(SLOTS, STAMPS)
     used = t[:, 0] != 0
+    if not used.any():
+        raise RuntimeError("no workgroup stamped: this launch did not use prefill_f16_kernel "
+                           "(the two-group kernel; longer prompts take the four-wave kernels)")
     t = t[used]
     t0 = t[:, 0].min()
     rel = np.where(t >= t0, (t.astype(np.float64) - float(t0)) * 0.01, np.nan)  # us
