@@ -157,8 +157,11 @@ template <> struct Kv8<BRASA_KV_Q8_0> {
 };
 
 // 16-byte HBM -> LDS copy per lane (global_load_lds_dwordx4): lane i writes lds + 16 i.
-// M0 (the LDS base) is saved and restored around it; an LDS-DMA load needs one wait state after
-// an SALU write of M0 (the s_nop), which the compiler cannot insert inside the asm. Issued as
+// M0 (the LDS base) is saved and restored around it. Wait states the compiler cannot insert
+// inside the asm: an LDS-DMA load needs one after an SALU write of M0, and a vector memory
+// instruction needs five after a VALU write (v_readfirstlane) of an SGPR it reads, here the
+// SGPR base of the _s variants, which the compiler may compute just before the asm: the two
+// s_mov and s_nop 2 give five. Issued as
 // inline asm so that the compiler's vector-memory counter bookkeeping never relies on it (its
 // own waits can only become more conservative); the wait before the LDS reads of such a tile
 // is wait_vmcnt below.
@@ -169,7 +172,7 @@ __device__ __forceinline__ void lds_dma16(const uint8_t* src, uint16_t* lds_wave
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %2\n\t"
-        "s_nop 0\n\t"
+        "s_nop 2\n\t"
         "global_load_lds_dwordx4 %1, off\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
@@ -184,7 +187,7 @@ __device__ __forceinline__ void lds_dma16_nt(const uint8_t* src, uint16_t* lds_w
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %2\n\t"
-        "s_nop 0\n\t"
+        "s_nop 2\n\t"
         "global_load_lds_dwordx4 %1, off nt\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
@@ -206,7 +209,7 @@ __device__ __forceinline__ void lds_dma16_s(const uint8_t* sbase, uint32_t voff,
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %3\n\t"
-        "s_nop 0\n\t"
+        "s_nop 2\n\t"
         "global_load_lds_dwordx4 %1, %2\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
@@ -220,7 +223,7 @@ __device__ __forceinline__ void lds_dma16_s_nt(const uint8_t* sbase, uint32_t vo
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %3\n\t"
-        "s_nop 0\n\t"
+        "s_nop 2\n\t"
         "global_load_lds_dwordx4 %1, %2 nt\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
@@ -234,7 +237,7 @@ __device__ __forceinline__ void lds_dma4_s_nt(const uint8_t* sbase, uint32_t vof
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %3\n\t"
-        "s_nop 0\n\t"
+        "s_nop 2\n\t"
         "global_load_lds_dword %1, %2 nt\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)

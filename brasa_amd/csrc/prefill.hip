@@ -502,15 +502,22 @@ __device__ __forceinline__ bool merge_key_parts(const PrefillArgs& a, int tile, 
     // of loads below is followed by s_waitcnt vmcnt(0) and an asm that names the loaded
     // registers, which keeps any use of them (or reuse of those registers) after the wait.
     // maximum over the parts, then the weighted sums in part order
+    // every slot gets a real load (parts past kparts and the own part read the own state,
+    // unused): selecting between a load's result and another value before the wait would copy
+    // the register before the data lands
+    f32x4 ld[kMaxKeyParts];
+#pragma unroll
+    for (int p = 0; p < kMaxKeyParts; ++p)
+        ld[p] = ld_dev16(state(p < a.kparts && p != part ? p : part) + 16 * 256);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int p = 0; p < kMaxKeyParts; ++p) asm volatile("" : "+v"(ld[p]));
     f32x4 ml[kMaxKeyParts];
 #pragma unroll
     for (int p = 0; p < kMaxKeyParts; ++p)
-        ml[p] = p == part       ? f32x4{m_used, lsum, 0.0f, 0.0f}
-                : p < a.kparts  ? ld_dev16(state(p) + 16 * 256)
-                                : f32x4{-INFINITY, 0.0f, 0.0f, 0.0f};
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#pragma unroll
-    for (int p = 0; p < kMaxKeyParts; ++p) asm volatile("" : "+v"(ml[p]));
+        ml[p] = p == part ? f32x4{m_used, lsum, 0.0f, 0.0f}
+                : p < a.kparts ? ld[p]
+                               : f32x4{-INFINITY, 0.0f, 0.0f, 0.0f};
     float M = -INFINITY;
 #pragma unroll
     for (int p = 0; p < kMaxKeyParts; ++p)
