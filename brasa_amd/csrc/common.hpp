@@ -157,11 +157,9 @@ template <> struct Kv8<BRASA_KV_Q8_0> {
 };
 
 // 16-byte HBM -> LDS copy per lane (global_load_lds_dwordx4): lane i writes lds + 16 i.
-// M0 (the LDS base) is saved and restored around it. Wait states the compiler cannot insert
-// inside the asm: an LDS-DMA load needs one after an SALU write of M0, and a vector memory
-// instruction needs five after a VALU write (v_readfirstlane) of an SGPR it reads, here the
-// SGPR base of the _s variants, which the compiler may compute just before the asm: the two
-// s_mov and s_nop 2 give five. Issued as
+// M0 (the LDS base) is saved and restored around it. An LDS-DMA load needs a wait state after
+// an SALU write of M0, which the compiler cannot insert inside the asm (the s_nop). The SGPR
+// base of the _s variants comes from sgpr_offset (an SALU write). Issued as
 // inline asm so that the compiler's vector-memory counter bookkeeping never relies on it (its
 // own waits can only become more conservative); the wait before the LDS reads of such a tile
 // is wait_vmcnt below.
@@ -194,15 +192,36 @@ __device__ __forceinline__ void lds_dma16_nt(const uint8_t* src, uint16_t* lds_w
         : "v"(src), "s"(m0)
         : "memory");
 }
-// A uniform 64-bit address as the SGPR pair an `s` asm operand needs (readfirstlane of both
-// halves: free when the compiler already holds it in SGPRs).
-__device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* p) {
+// Uniform 64-bit addresses as the SGPR pairs the _s copy helpers read. The compiler may hold
+// a uniform value in VGPRs and move it to SGPRs with v_readfirstlane (a VALU write of the SGPRs)
+// just before the copy. On gfx950 a vector memory instruction that read the SGPRs 5 wait states
+// after that write copied from a wrong base now and then (q8_0 decode at 16K keys: whole KV
+// heads wrong or NaN in most calls); with 18 wait states no call in 24 was.
+// sgpr_base: once per kernel for a cache base; the asm that holds the SGPRs pads 18 wait states
+// after their write.
+__device__ __forceinline__ const uint8_t* sgpr_base(const uint8_t* p) {
     const uint64_t v = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 1" : "+s"(lo), "+s"(hi));
     return reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
 }
-// As lds_dma16 with a uniform 64-bit base in SGPRs and a per-lane 32-bit byte offset.
+// sgpr_offset: a block's address, base (from sgpr_base) + a uniform byte offset, summed by SALU
+// instructions in the asm, so the copies read SGPRs no VALU instruction wrote (a VALU write of
+// the offset's SGPRs read by those SALU instructions needs no wait states).
+__device__ __forceinline__ const uint8_t* sgpr_offset(const uint8_t* sbase, uint64_t off) {
+    const uint64_t b = reinterpret_cast<uint64_t>(sbase);
+    const uint32_t olo = __builtin_amdgcn_readfirstlane((uint32_t)off);
+    const uint32_t ohi = __builtin_amdgcn_readfirstlane((uint32_t)(off >> 32));
+    uint32_t lo, hi;
+    asm volatile("s_add_u32 %0, %2, %4\n\ts_addc_u32 %1, %3, %5"
+                 : "=&s"(lo), "=&s"(hi)
+                 : "s"((uint32_t)b), "s"((uint32_t)(b >> 32)), "s"(olo), "s"(ohi)
+                 : "scc");
+    return reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
+}
+// As lds_dma16 with a uniform 64-bit base in SGPRs (from sgpr_offset) and a per-lane 32-bit
+// byte offset.
 __device__ __forceinline__ void lds_dma16_s(const uint8_t* sbase, uint32_t voff,
                                             uint32_t lds_wave_base /* uniform LDS address */) {
     uint32_t saved;
@@ -213,7 +232,7 @@ __device__ __forceinline__ void lds_dma16_s(const uint8_t* sbase, uint32_t voff,
         "global_load_lds_dwordx4 %1, %2\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
-        : "v"(voff), "s"(uniform_ptr(sbase)), "s"(lds_wave_base)
+        : "v"(voff), "s"(sbase), "s"(lds_wave_base)
         : "memory");
 }
 // As lds_dma16_s with the nontemporal hint.
@@ -227,7 +246,7 @@ __device__ __forceinline__ void lds_dma16_s_nt(const uint8_t* sbase, uint32_t vo
         "global_load_lds_dwordx4 %1, %2 nt\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
-        : "v"(voff), "s"(uniform_ptr(sbase)), "s"(lds_wave_base)
+        : "v"(voff), "s"(sbase), "s"(lds_wave_base)
         : "memory");
 }
 // 4-byte variant of lds_dma16_s_nt (lane i writes lds + 4 i).
@@ -241,7 +260,7 @@ __device__ __forceinline__ void lds_dma4_s_nt(const uint8_t* sbase, uint32_t vof
         "global_load_lds_dword %1, %2 nt\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
-        : "v"(voff), "s"(uniform_ptr(sbase)), "s"(lds_wave_base)
+        : "v"(voff), "s"(sbase), "s"(lds_wave_base)
         : "memory");
 }
 // Device-coherent stores and loads (written through / read past the XCD's L2): a partial

@@ -941,8 +941,8 @@ decode_q8_kernel(DecodeArgs<NS> a) {
     const int nblk = (s1 - s0 + kBlock - 1) / kBlock;
     const int nb = (hg_ok && nblk > ks) ? (nblk - ks + KS - 1) / KS : 0;
     const size_t kstride = (size_t)a.hkv * RB;
-    const uint8_t* kbase = sd.k + (size_t)kh * RB;
-    const uint8_t* vbase = sd.v + (size_t)kh * RB;
+    const uint8_t* kbase = sgpr_base(sd.k + (size_t)kh * RB);
+    const uint8_t* vbase = sgpr_base(sd.v + (size_t)kh * RB);
 
     u32x4 qr[8];
     {
@@ -972,8 +972,8 @@ decode_q8_kernel(DecodeArgs<NS> a) {
         constexpr int S = decltype(slot_c)::value;
         const int jb = s0 + kBlock * (ks + KS * i);
         const uint32_t sl = lds_addr(&s_slot[wave][S][0]);
-        const uint8_t* kb = kbase + (size_t)jb * kstride;
-        const uint8_t* vb = vbase + (size_t)jb * kstride;
+        const uint8_t* kb = sgpr_offset(kbase, (size_t)jb * kstride);
+        const uint8_t* vb = sgpr_offset(vbase, (size_t)jb * kstride);
         if (jb + kBlock <= s1) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) lds_dma16_s_nt(kb, off_k[r], sl + 1024 * r);

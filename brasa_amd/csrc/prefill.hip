@@ -635,8 +635,8 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
         const int row = 16 * qw + 4 * r + lr;
         return (uint32_t)(row * rstride + 16 * vswz(row, lc));
     };
-    const uint8_t* kbase = a.k + (size_t)kh * 256;
-    const uint8_t* vbase = a.v + (size_t)kh * 256;
+    const uint8_t* kbase = sgpr_base(a.k + (size_t)kh * 256);
+    const uint8_t* vbase = sgpr_base(a.v + (size_t)kh * 256);
     // the 4 waves of a group copy 16 rows each of the group's tiles
     const uint32_t lds_k = lds_addr(&s_kv[0][grp][0][0]) + qw * 16 * 256;
     const uint32_t lds_v = lds_addr(&s_kv[1][grp][0][0]) + qw * 16 * 256;
@@ -651,12 +651,12 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
         vso[r] = vdo(r, lrow, lchunk);
     }
     auto dma_k = [&](int i) {
-        const uint8_t* g = kbase + (size_t)kb_of(i) * rstride;
+        const uint8_t* g = sgpr_offset(kbase, (size_t)kb_of(i) * rstride);
 #pragma unroll
         for (int r = 0; r < 4; ++r) lds_dma16_s(g, kso[r], lds_k + (i & 1) * kTileBytes + r * 1024);
     };
     auto dma_v = [&](int i) {
-        const uint8_t* g = vbase + (size_t)kb_of(i) * rstride;
+        const uint8_t* g = sgpr_offset(vbase, (size_t)kb_of(i) * rstride);
 #pragma unroll
         for (int r = 0; r < 4; ++r) lds_dma16_s(g, vso[r], lds_v + (i & 1) * kTileBytes + r * 1024);
     };
@@ -978,13 +978,13 @@ prefill_f16_kernel4(PrefillArgs a) {
             vdo[r] = row * rstride + 16 * vswz(row, lchunk);
         }
     }
-    const uint8_t* kbase = a.k + (size_t)kh * 256;
-    const uint8_t* vbase = a.v + (size_t)kh * 256;
+    const uint8_t* kbase = sgpr_base(a.k + (size_t)kh * 256);
+    const uint8_t* vbase = sgpr_base(a.v + (size_t)kh * 256);
     const uint32_t lds_k = lds_addr(&s_k[0][0]) + wave * 16 * 256;
     const uint32_t lds_v = lds_addr(&s_vv[0][0]) + wave * 16 * 256;
     auto dma = [&](int kb, int buf) {
-        const uint8_t* kg = kbase + (size_t)kb * rstride;
-        const uint8_t* vg = vbase + (size_t)kb * rstride;
+        const uint8_t* kg = sgpr_offset(kbase, (size_t)kb * rstride);
+        const uint8_t* vg = sgpr_offset(vbase, (size_t)kb * rstride);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             lds_dma16_s(kg, kdo[r], lds_k + buf * kTileBytes + r * 1024);
@@ -1374,8 +1374,8 @@ prefill_f16_kernel4s(PrefillArgs a) {
             voff[dt] = (4 * u + j) * 256 + 16 * (4 * (dt ^ j) + low) + 8 * (sl & 1);
     }
     const uint32_t rstride = (uint32_t)a.hkv * 256;
-    const uint8_t* kbase = a.k + (size_t)kh * 256;
-    const uint8_t* vbase = a.v + (size_t)kh * 256;
+    const uint8_t* kbase = sgpr_base(a.k + (size_t)kh * 256);
+    const uint8_t* vbase = sgpr_base(a.v + (size_t)kh * 256);
     // each wave copies 8 rows of a 32-key stage: rows 8 wave + 4 r + lane / 16
     const uint32_t lds_k = lds_addr(&s_k[0][0]) + wave * 8 * 256;
     const uint32_t lds_v = lds_addr(&s_vv[0][0]) + wave * 8 * 256;
@@ -1388,8 +1388,8 @@ prefill_f16_kernel4s(PrefillArgs a) {
         vso[r] = (uint32_t)(row * rstride + 16 * vswz(row, lc));
     }
     auto dma = [&](int kb, int buf) {
-        const uint8_t* kg = kbase + (size_t)kb * rstride;
-        const uint8_t* vg = vbase + (size_t)kb * rstride;
+        const uint8_t* kg = sgpr_offset(kbase, (size_t)kb * rstride);
+        const uint8_t* vg = sgpr_offset(vbase, (size_t)kb * rstride);
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
             lds_dma16_s(kg, kso[r], lds_k + buf * kTileBytes + r * 1024);
