@@ -79,10 +79,14 @@ def copy_base_hazards(asm: str) -> tuple[int, list[str]]:
                 ws += int(parts[1], 0) + 1
                 continue
             ops_j = parts[1].split(",") if len(parts) > 1 else []
-            if _written(mn, ops_j) & want and not mn.startswith(("global_", "buffer_", "s_waitcnt")):
+            hit = _written(mn, ops_j) & want
+            if hit and not mn.startswith(("global_", "buffer_", "s_waitcnt")):
                 if mn.startswith("v_") and ws < MIN_WAIT_STATES:
                     bad.append(f"{fn}: line {i + 1} `{line}` <- `{t}` after {ws} wait states")
-                break
+                    break
+                want = want - hit  # each register's last writer decides for it
+                if not want:
+                    break
             ws += 1
     return n, bad
 
@@ -114,7 +118,8 @@ def test_copy_bases_not_fresh_valu_writes(kernels_asm, src):
 
 def test_scan_flags_a_fresh_readfirstlane():
     """The scan itself: a base written by v_readfirstlane 5 wait states before the copy is
-    flagged, the same base with 18 is not, and an SALU-written base is not."""
+    flagged, the same base with 18 is not, an SALU-written base is not, and a pair with one
+    half written by each is."""
     fresh = """_Zk:
     v_readfirstlane_b32 s3, v37
     v_readfirstlane_b32 s2, v36
@@ -130,6 +135,11 @@ def test_scan_flags_a_fresh_readfirstlane():
     s_addc_u32 s3, s5, s7
     global_load_lds_dwordx4 v75, s[2:3] nt
 """
+    split = """_Zk:
+    v_readfirstlane_b32 s2, v36
+    s_mov_b32 s3, s9
+    global_load_lds_dwordx4 v75, s[2:3] nt
+"""
     carry = """_Zk:
     v_mad_u64_u32 v[34:35], s[2:3], s10, v34, v[122:123]
     global_load_lds_dword v75, s[2:3]
@@ -138,4 +148,5 @@ def test_scan_flags_a_fresh_readfirstlane():
     assert n == 1 and len(bad) == 1
     assert copy_base_hazards(padded) == (1, [])
     assert copy_base_hazards(salu) == (1, [])
+    assert len(copy_base_hazards(split)[1]) == 1
     assert len(copy_base_hazards(carry)[1]) == 1
