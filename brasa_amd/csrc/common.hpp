@@ -69,6 +69,20 @@ __device__ __forceinline__ void codes4_to_f16(uint32_t w, uint32_t& lo, uint32_t
     hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, h) + bias);
 }
 
+// As codes4_to_f16 with the values scaled by 2^e, -14 <= e <= 5: the magic's exponent byte
+// ebyte = 4 (e + 25) (in every byte) encodes 2^e (1024 + code + 128), and bias = -1152 * 2^e
+// (a normal f16 in that range) leaves code * 2^e, exact (7 significant bits, >= 2^-14 steps).
+__device__ __forceinline__ void codes4_to_f16_exp(uint32_t w, uint32_t ebyte, uint32_t bias,
+                                                  uint32_t& lo, uint32_t& hi) {
+    const uint32_t x = w ^ 0x80808080u;
+    const uint32_t l = __builtin_amdgcn_perm(ebyte, x, 0x04010400u);  // [e, b1, e, b0]
+    const uint32_t h = __builtin_amdgcn_perm(ebyte, x, 0x04030402u);  // [e, b3, e, b2]
+    typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+    const half2 b = __builtin_bit_cast(half2, bias);
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, l) + b);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, h) + b);
+}
+
 // ---- DPP / cross-lane helpers (wave64) ----------------------------------------------------
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {

@@ -256,13 +256,18 @@ struct F32Block {
     F32Chunk v[8];
 };
 
-// A q8_0 scale s is applied as 2^e * (s * 2^-e), e = min(exponent(s), 9) (-14 for f16
-// subnormals): 2^e goes into the f16 V codes (code * 2^e is exact in f16 for |code| <= 127) and
-// the mantissa part into P, so P * mantissa keeps its hi/lo split clear of f16 subnormals.
+// A q8_0 scale s is applied as 2^e * (s * 2^-e), e = min(exponent(s), 5) (-14 for f16
+// subnormals): 2^e goes into the f16 V codes (code * 2^e, exact, made by the conversion itself,
+// codes4_to_f16_exp) and the rest m = s * 2^-e into P. m < 2 up to s < 64 and m < 2^11 above;
+// with P <= 2^kLazyRescaleQ8 = 16 the product stays below 2^15 (f16 range), and its hi/lo split
+// stays clear of f16 subnormals for m >= 2^-10.
 __device__ __forceinline__ int q8_exp(uint16_t sc) {
     const int e = (int)((sc >> 10) & 31u);
-    return e == 0 ? -14 : min(e - 15, 9);
+    return e == 0 ? -14 : min(e - 15, 5);
 }
+// Row r's 16-byte V-code chunk c sits at chunk c ^ q8_vswz(r) of the row in LDS: the conversion's
+// 16-byte reads (lane 2 r + h reads chunk 4 h + j of row r) then hit distinct bank groups.
+__device__ __forceinline__ int q8_vswz(int r) { return (r ^ (r >> 2)) & 3; }
 
 // ---- the end of a split: merge the W waves, then the splits --------------------------------
 // (M, A, L) <- merge of (M, A, L) and (m, a, l): M = max, weights 2^(m - M) (0 for an empty side)
@@ -647,6 +652,7 @@ constexpr int kRing = 2;                    // blocks in flight per wave (16 ins
 constexpr int kMaxLdsWaves = 8;
 constexpr int kTileHalves = kBlock * kDim;  // one 32 x 128 f16 tile = 8 KB
 constexpr float kLazyRescale = 8.0f;        // log2 of the largest P value before a rescale
+constexpr float kLazyRescaleQ8 = 4.0f;      // the same for the q8_0 kernel (P * m in f16 range)
 
 __device__ __forceinline__ u32x4 ld16_asm(const uint8_t* p) {
     u32x4 r;
@@ -764,14 +770,14 @@ decode_f16_kernel(DecodeArgs<NS> a) {
     };
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    if (nb > 0) issue(I0{}, 0);
-    if (nb > 1) issue(I1{}, 1);
-    // Q was issued first: it has landed when at most the blocks' instructions are pending
-    switch (min(nb, kRing)) {
-        case 2: wait_k<32>(qr); break;
-        case 1: wait_k<16>(qr); break;
-        default: wait_k<0>(qr); break;
-    }
+    // Both ring slots are always filled (a wave with fewer blocks gets rows clamped to the
+    // split's last one, never read), so one wait with a fixed count follows the Q loads in
+    // straight-line code: Q was issued first, so it has landed when at most the blocks'
+    // instructions are pending. (A wait chosen by a branch let the compiler copy the Q registers
+    // in one arm before the wait, reading them while the loads were still in flight.)
+    issue(I0{}, 0);
+    issue(I1{}, 1);
+    wait_k<32>(qr);
 
     // ---- Q^T B-operand: k-step t holds dims 32 t + 8 u + j; column c < G: head h0 + c, hi half;
     // G <= c < 2 G: the same head, lo half; other columns zero ------------------------------------
@@ -869,6 +875,11 @@ decode_f16_kernel(DecodeArgs<NS> a) {
         if (i0 + 1 >= nb) break;
         step(I1{}, i0 + 1);
     }
+    // a slot filled for a block past nb was never waited for by a step: wait and name its
+    // registers, so none of them is reused while its loads are in flight (no-op after a last
+    // step, which waits for everything)
+    wait_k<0>(kr[0]);
+    wait_k<0>(kr[1]);
 
     // ---- the split's end ---------------------------------------------------------------------
     lsum = sum_rows(lsum);
@@ -890,18 +901,21 @@ decode_f16_kernel(DecodeArgs<NS> a) {
 }
 
 // ---- q8_0 caches: the f16 kernel's structure with codes and scales staged in LDS -----------
-// Same workgroup layout, plan, ring, explicit waits and split merge as decode_f16_kernel. A ring
-// slot holds one 32-key block of K and V in their storage form: codes (32 x 128 bytes each) and
-// the 4 f16 scales per row (32 x 8 bytes each), copied by 16-byte (codes) and 4-byte (scales)
-// global_load_lds; 10 copy instructions per block.
+// Same workgroup layout, plan, explicit waits and split merge as decode_f16_kernel; two LDS slots
+// per wave, but a wave issues block i + 1 only once block i has landed. A slot holds one 32-key
+// block of K and V in their storage form: codes (32 x 128 bytes each) and the 4 f16 scales per
+// row (32 x 8 bytes each), copied by 16-byte (codes) and 4-byte (scales) global_load_lds; 10
+// copy instructions per block.
 //  * S^T = K Q^T: K codes are read in the MFMA A layout (16-byte chunk c of row r stored at
 //    c ^ ((r >> 1) & 7): conflict-free 8-byte reads), converted exactly to f16, and each 32-dim
 //    group (one MFMA k-step) gets its own accumulator, scaled by that row's group scale in f32:
 //    s = sum_g scale_g * (q . codes_g), the exact dequantised dot product up to f32 rounding.
-//  * O^T += V^T P^T: after the block's S, each lane converts 64 V codes to f16 times 2^e (exact:
-//    |code| <= 127, e <= 9) and writes them as the f16 V tile over the block's code area (the
-//    ds_read_tr16_b64 layout of the f16 kernel); the scale's mantissa factor scale * 2^-e is
-//    folded into P per 32-dim group, so every product stays exact up to the f32 accumulation.
+//  * O^T += V^T P^T: after the block's S, each lane converts 64 V codes (V rows stored with
+//    chunk c of row r at c ^ q8_vswz(r)) to f16 times 2^e (exact: |code| <= 127, -14 <= e <= 5,
+//    the 2^e built into the conversion's magic number) and writes them as the f16 V tile over
+//    the block's code area (the ds_read_tr16_b64 layout of the f16 kernel); the rest of the
+//    scale, scale * 2^-e, is folded into P per 32-dim group, so every product stays exact up to
+//    the f32 accumulation.
 constexpr int kQ8Codes = kBlock * 128;        // bytes of one tile's codes
 constexpr int kQ8Fac = 2 * kQ8Codes + 2 * kBlock * 8;   // K codes, V codes, K scales, V scales,
 constexpr int kQ8Slot = kQ8Fac + kBlock * 4 * 4;         // then V mantissa factors [key][group]
@@ -965,12 +979,12 @@ decode_q8_kernel(DecodeArgs<NS> a) {
     for (int r = 0; r < 4; ++r) {
         const int rr = 8 * r + lr;
         off_k[r] = (uint32_t)(rr * kstride) + 16 * (lc ^ ((rr >> 1) & 7));
-        off_v[r] = (uint32_t)(rr * kstride) + 16 * lc;
+        off_v[r] = (uint32_t)(rr * kstride) + 16 * (lc ^ q8_vswz(rr));
     }
     const uint32_t off_s = (uint32_t)(sr * kstride) + 128 + 4 * (lane & 1);
-    auto issue = [&](auto slot_c, int i) {
+    // block starting at key jb (s0 <= jb < s1) -> slot S
+    auto issue_at = [&](auto slot_c, int jb) {
         constexpr int S = decltype(slot_c)::value;
-        const int jb = s0 + kBlock * (ks + KS * i);
         const uint32_t sl = lds_addr(&s_slot[wave][S][0]);
         const uint8_t* kb = sgpr_offset(kbase, (size_t)jb * kstride);
         const uint8_t* vb = sgpr_offset(vbase, (size_t)jb * kstride);
@@ -991,23 +1005,27 @@ decode_q8_kernel(DecodeArgs<NS> a) {
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const uint32_t row = (uint32_t)(min(8 * r + lr, last) * kstride);
-                lds_dma16_s_nt(vb, row + 16 * lc, sl + kQ8Codes + 1024 * r);
+                const int rr = 8 * r + lr;
+                const uint32_t row = (uint32_t)(min(rr, last) * kstride);
+                lds_dma16_s_nt(vb, row + 16 * (lc ^ q8_vswz(rr)), sl + kQ8Codes + 1024 * r);
             }
             const uint32_t srow = (uint32_t)(min(sr, last) * kstride) + 128 + 4 * (lane & 1);
             lds_dma4_s_nt(kb, srow, sl + 2 * kQ8Codes);
             lds_dma4_s_nt(vb, srow, sl + 2 * kQ8Codes + 256);
         }
     };
+    auto issue = [&](auto slot_c, int i) { issue_at(slot_c, s0 + kBlock * (ks + KS * i)); };
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    if (nb > 0) issue(I0{}, 0);
-    if (nb > 1) issue(I1{}, 1);
-    switch (min(nb, kRing)) {
-        case 2: wait_k<20>(qr); break;
-        case 1: wait_k<10>(qr); break;
-        default: wait_k<0>(qr); break;
-    }
+    // The prologue always issues one block (a wave without blocks copies the split's first one,
+    // never read), so one wait with a fixed count follows the Q loads in straight-line code.
+    // (A wait chosen by a branch let the compiler copy the Q registers in one arm before the
+    // wait, reading them while the loads were in flight.) Block i + 1 is issued once block i
+    // has landed (in step i): with one block per wave in flight at the start, the first blocks
+    // land earlier and block i's math overlaps block i + 1's copies (18.6 -> 18.3 us per layer
+    // at 16K keys).
+    issue_at(I0{}, nb > 0 ? s0 + kBlock * ks : s0);
+    wait_k<10>(qr);
 
     half8 qb[4];
     {
@@ -1036,8 +1054,12 @@ decode_q8_kernel(DecodeArgs<NS> a) {
 
     auto step = [&](auto slot_c, int i) {
         constexpr int S = decltype(slot_c)::value;
-        if (i + 1 < nb) wait_vmcnt<10>();
-        else wait_vmcnt<0>();
+        wait_vmcnt<0>();  // block i: the only copies in flight
+        if (i + 1 < nb) {
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the other slot's reads returned
+            asm volatile("" ::: "memory");
+            issue(std::integral_constant<int, 1 - S>{}, i + 1);
+        }
         if (i == 0) DECODE_STAMP(kStampFirstBlock);
         if (i + 1 == nb) DECODE_STAMP(kStampLastBlock);
         const int jb = s0 + kBlock * (ks + KS * i);
@@ -1082,7 +1104,7 @@ decode_q8_kernel(DecodeArgs<NS> a) {
                 bm = fmaxf(bm, x[kt][r]);
             }
         bm = max_rows(bm);
-        if (__builtin_amdgcn_ballot_w64(bm > mref + kLazyRescale) != 0) {
+        if (__builtin_amdgcn_ballot_w64(bm > mref + kLazyRescaleQ8) != 0) {
             const float mn = fmaxf(mref, bm);
             const float alpha = __builtin_amdgcn_exp2f(mref - mn);
             mref = mn;
@@ -1105,7 +1127,8 @@ decode_q8_kernel(DecodeArgs<NS> a) {
             u32x4 vc[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                vc[j] = *reinterpret_cast<const u32x4*>(sl + kQ8Codes + vr * 128 + 64 * vh + 16 * j);
+                vc[j] = *reinterpret_cast<const u32x4*>(sl + kQ8Codes + vr * 128 +
+                                                        16 * ((4 * vh + j) ^ q8_vswz(vr)));
             const uint32_t vs = *reinterpret_cast<const uint32_t*>(vsc + vr * 8 + 4 * vh);
             const uint16_t sc2[2] = {(uint16_t)(vs & 0xffffu), (uint16_t)(vs >> 16)};
             int ex[2];
@@ -1119,20 +1142,22 @@ decode_q8_kernel(DecodeArgs<NS> a) {
             asm volatile("" ::: "memory");
             *reinterpret_cast<f32x2*>(fac + vr * 4 + 2 * vh) = f32x2{fm[0], fm[1]};
             uint16_t* vt = reinterpret_cast<uint16_t*>(sl);
+            // per group: the conversion magic's exponent byte and bias for 2^e (codes4_to_f16_exp)
+            uint32_t eb[2], bias[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                eb[q] = (uint32_t)(4 * (ex[q] + 25)) * 0x01010101u;
+                const uint32_t b16 = (uint32_t)__builtin_bit_cast(
+                    uint16_t, (_Float16)__builtin_amdgcn_ldexpf(-1152.0f, ex[q]));
+                bias[q] = b16 | (b16 << 16);
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                typedef _Float16 half2 __attribute__((ext_vector_type(2)));
-                const _Float16 p2 = (_Float16)__builtin_amdgcn_ldexpf(1.0f, ex[j >> 1]);
-                const half2 m2 = {p2, p2};
                 const uint32_t w[4] = {vc[j].x, vc[j].y, vc[j].z, vc[j].w};
                 uint32_t hv[8];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    uint32_t l, h;
-                    codes4_to_f16(w[e], l, h);
-                    hv[2 * e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, l) * m2);      // exact
-                    hv[2 * e + 1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, h) * m2);
-                }
+                for (int e = 0; e < 4; ++e)
+                    codes4_to_f16_exp(w[e], eb[j >> 1], bias[j >> 1], hv[2 * e], hv[2 * e + 1]);
                 // 16 codes = dims 64 vh + 16 j .. + 16: logical chunks 8 vh + 2 j, + 1 of row vr
 #pragma unroll
                 for (int q = 0; q < 2; ++q) {
@@ -1170,17 +1195,13 @@ decode_q8_kernel(DecodeArgs<NS> a) {
             const half8 va = __builtin_bit_cast(half8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
             acc[dt] = mfma16(va, pb[dt >> 1], acc[dt]);
         }
-        if (i + kRing < nb) {
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the slot's reads have returned
-            asm volatile("" ::: "memory");
-            issue(slot_c, i + kRing);
-        }
     };
     for (int i0 = 0; i0 < nb; i0 += kRing) {
         step(I0{}, i0);
         if (i0 + 1 >= nb) break;
         step(I1{}, i0 + 1);
     }
+    wait_vmcnt<0>();  // copies of a wave without blocks land before the LDS is reused below
 
     // ---- the split's end ---------------------------------------------------------------------
     lsum = sum_rows(lsum);

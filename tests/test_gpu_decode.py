@@ -141,6 +141,28 @@ def test_decode_scratch_too_small():
     assert e.value.code == 2
 
 
+@pytest.mark.parametrize("vscale", [40.0, 3e3, 2.7e6])
+def test_decode_q8_large_v_scales(vscale):
+    """q8_0 V groups with scales from ~1 up to ~6.4e4 (near the f16 maximum): the part of a scale
+    above 2^5 stays in the factor folded into P, which must neither overflow f16 nor lose
+    precision; the result holds the 1e-5 bar relative to max|v|."""
+    k = Kernels()
+    rng = oracle.Rng(58)
+    for pos0 in [300, 4095]:
+        lk = pos0 + 1
+        q = rng.vec(HQ * DIM, 2.0)
+        kv_k = rng.vec(lk * HKV * DIM, 2.0)
+        kv_v = rng.vec(lk * HKV * DIM, 3.0) * np.float32(vscale)
+        cache = KvPair(KvType.Q8_0, kv_k, kv_v)
+        assert np.isfinite(cache.v).all()
+        _say(f"decode q8 large V scales {vscale} pos0={pos0}")
+        got = run_decode(k, "lanes", q, cache, HQ, HKV, pos0)
+        want, vmax = oracle.attention(q, cache.k, cache.v, 1, HQ, HKV, DIM, pos0)
+        w = oracle.worst(got, want, vmax)
+        print(f"q8 V scale {vscale} pos0 {pos0}: max |v| {np.abs(cache.v).max():.3g}, worst {w:.2e}")
+        assert w <= 1e-5, w
+
+
 @pytest.mark.parametrize("vscale", [1e-3, 1e-4, 3e-6])
 def test_decode_q8_small_scales(vscale):
     """q8_0 caches whose group scales are small or f16-subnormal (|v| ~ vscale): the dequantised
