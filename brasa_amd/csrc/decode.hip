@@ -770,14 +770,14 @@ decode_f16_kernel(DecodeArgs<NS> a) {
     };
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    // Both ring slots are always filled (a wave with fewer blocks gets rows clamped to the
-    // split's last one, never read), so one wait with a fixed count follows the Q loads in
-    // straight-line code: Q was issued first, so it has landed when at most the blocks'
-    // instructions are pending. (A wait chosen by a branch let the compiler copy the Q registers
-    // in one arm before the wait, reading them while the loads were still in flight.)
-    issue(I0{}, 0);
-    issue(I1{}, 1);
-    wait_k<32>(qr);
+    if (nb > 0) issue(I0{}, 0);
+    if (nb > 1) issue(I1{}, 1);
+    // Q was issued first: it has landed when at most the blocks' instructions are pending
+    switch (min(nb, kRing)) {
+        case 2: wait_k<32>(qr); break;
+        case 1: wait_k<16>(qr); break;
+        default: wait_k<0>(qr); break;
+    }
 
     // ---- Q^T B-operand: k-step t holds dims 32 t + 8 u + j; column c < G: head h0 + c, hi half;
     // G <= c < 2 G: the same head, lo half; other columns zero ------------------------------------
@@ -875,11 +875,6 @@ decode_f16_kernel(DecodeArgs<NS> a) {
         if (i0 + 1 >= nb) break;
         step(I1{}, i0 + 1);
     }
-    // a slot filled for a block past nb was never waited for by a step: wait and name its
-    // registers, so none of them is reused while its loads are in flight (no-op after a last
-    // step, which waits for everything)
-    wait_k<0>(kr[0]);
-    wait_k<0>(kr[1]);
 
     // ---- the split's end ---------------------------------------------------------------------
     lsum = sum_rows(lsum);

@@ -159,6 +159,11 @@ def _inflight_uses(lines: list, maxdepth: int = 64) -> dict:
             if w[0] == "s_branch":
                 s.append(index.get(w[1]))
                 fall = False
+            elif w[0] == "s_cbranch_execz":
+                # taken only when no lane would run the skipped code: for the uniform conditions
+                # of these kernels the code is then a no-op, so only the fall-through is followed
+                # (the pending loads can only be overcounted)
+                pass
             elif w[0].startswith("s_cbranch"):
                 s.append(index.get(w[1]))
             elif w[0] == "s_endpgm":
