@@ -55,6 +55,7 @@ SYMBOLS = {
     "brasa_qk_norm_rope_store": (INT, [INT, VP, VP, VP, VP, VP, ctypes.c_float, RopeTableC, VP,
                                        VP, AttnShapeC, VP]),
     "brasa_test_set_prefill_layout": (INT, [INT, INT, INT]),
+    "brasa_release_workspaces": (INT, []),
     "brasa_last_error": (ctypes.c_char_p, []),
     "brasa_version": (ctypes.c_char_p, []),
     "brasa_rt_device_count": (INT, [ctypes.POINTER(INT)]),

@@ -34,6 +34,7 @@ int decode_batch_launch(const float* q, const void* const* k, const void* const*
 int prefill_launch(const float* q, const void* k, const void* v, void* o, int tokens, int hq,
                    int hkv, int pos0, int kv, int precision, hipStream_t stream);
 void prefill_set_layout(int variant, int pair, int parts);
+int prefill_release_workspaces();
 
 namespace {
 thread_local char g_err[512] = "";
@@ -299,6 +300,11 @@ int brasa_qk_norm_rope_store(int kv, float* q, float* k, const float* v, const f
     return qk_norm_rope_store_launch(kv, q, k, v, q_norm, k_norm, eps, table.cos, table.sin,
                                      k_dst, v_dst, s.tokens, s.hq, s.hkv, s.pos0,
                                      as_stream(stream));
+}
+
+int brasa_release_workspaces(void) {
+    g_err[0] = 0;
+    return prefill_release_workspaces();
 }
 
 int brasa_test_set_prefill_layout(int variant, int pair, int parts) {

@@ -27,6 +27,7 @@
 //     phases alternate; up to two workgroups per CU), prefill_f16_kernel4 (4 waves, two per CU)
 //     and prefill_f16_kernel4s (4 waves on 32-key stages, three per CU).
 #include <atomic>
+#include <map>
 #include <mutex>
 #include <type_traits>
 
@@ -1524,6 +1525,7 @@ std::atomic<int> g_force_variant{0};  // 0: chosen by size; 1, 2, 4: the kernels
 std::atomic<int> g_allow_pair{1};
 std::atomic<int> g_force_parts{1};    // key parts of a forced prefill_f16_kernel launch
 
+
 // Arrival counters of the key-split merge: one per (query tile, wave), 64 bytes apart, in
 // kPfCounterSlots slots taken round robin per launch; zero at load, returned to zero by every
 // launch (the last arrival wraps them).
@@ -1533,6 +1535,55 @@ __device__ unsigned g_pf_arrivals[kPfCounterSlots * kPfSlotWords];
 std::atomic<unsigned> g_pf_next_slot{0};
 unsigned* g_pf_ctr_base[64];
 std::once_flag g_pf_ctr_once[64];
+
+// Workspaces (key-split partials, q8_0 staging): one cached buffer per (device, stream, kind),
+// grown with hipMallocAsync / hipFreeAsync on that stream when a call needs more and otherwise
+// reused as it is. Calls on one stream run in order, so a stream's buffer is never used by two
+// launches at once; calls on different streams get different buffers. (An allocation and a
+// free per call cost ~5.7 us of idle GPU between launches, from the default pool and from a
+// pool that keeps its memory alike.) Held until brasa_release_workspaces() or process exit.
+enum WsKind { kWsKeySplit = 0, kWsQ8Staging = 1 };
+struct WsKey {
+    int dev;
+    hipStream_t stream;
+    int kind;
+    bool operator<(const WsKey& o) const {
+        if (dev != o.dev) return dev < o.dev;
+        if (stream != o.stream) return stream < o.stream;
+        return kind < o.kind;
+    }
+};
+struct WsBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mu;
+std::map<WsKey, WsBuf> g_ws;
+
+hipError_t workspace(WsKind kind, size_t bytes, hipStream_t stream, void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    WsBuf& b = g_ws[WsKey{dev, stream, kind}];
+    if (b.bytes < bytes) {
+        const size_t grow = (bytes + (2u << 20) - 1) / (2u << 20) * (2u << 20);  // 2 MiB steps
+        if (b.p) {
+            e = hipFreeAsync(b.p, stream);
+            b.p = nullptr;
+            b.bytes = 0;
+            if (e != hipSuccess) return e;
+        }
+        e = hipMallocAsync(&b.p, grow, stream);
+        if (e != hipSuccess) {
+            b.p = nullptr;
+            return e;
+        }
+        b.bytes = grow;
+    }
+    *out = b.p;
+    return hipSuccess;
+}
 
 // Key parts per query tile: 1 (no split) unless the launch fills at most half of the
 // workgroup slots (`slots`: CUs x workgroups per CU of the kernel) and the tiles' keys are long
@@ -1563,21 +1614,45 @@ int launch_split(K kernel, const char* name, PrefillArgs b, int hw, long long wg
     const unsigned slot = g_pf_next_slot.fetch_add(1, std::memory_order_relaxed) % kPfCounterSlots;
     void* ws = nullptr;
     const size_t bytes = (size_t)wgs * parts * kKeyPartFloats * sizeof(float);
-    hipError_t e = hipMallocAsync(&ws, bytes, stream);
+    hipError_t e = workspace(kWsKeySplit, bytes, stream, &ws);
     if (e != hipSuccess)
-        return set_error(BRASA_ERR_LAUNCH, "flash_attention: hipMallocAsync(%zu): %s", bytes,
-                         hipGetErrorString(e));
+        return set_error(BRASA_ERR_LAUNCH, "flash_attention: workspace allocation (%zu bytes): %s",
+                         bytes, hipGetErrorString(e));
     b.pair = 0;
     b.kparts = parts;
     b.part = static_cast<float*>(ws);
     b.ctr = g_pf_ctr_base[dev] + (size_t)slot * kPfSlotWords;
     hipLaunchKernelGGL(kernel, dim3(b.hq / hw, b.ntiles * parts), dim3(threads), 0, stream, b);
-    const int st = check_launch(name);
-    e = hipFreeAsync(ws, stream);
-    if (st != BRASA_OK) return st;
-    if (e != hipSuccess)
-        return set_error(BRASA_ERR_LAUNCH, "flash_attention: hipFreeAsync: %s", hipGetErrorString(e));
-    return BRASA_OK;
+    return check_launch(name);
+}
+
+// q8_0 rows -> f16 rows [rows, 128], each value f16(code * scale) by the same packed f16 multiply
+// as prefill_q8_kernel4 (bit-identical values). One thread per 16-code chunk (two 8-byte code
+// loads and the chunk's scale; 136-byte rows are 8-byte aligned); grid y: K, V.
+__global__ void __launch_bounds__(256)
+dequant_q8_f16_kernel(const uint8_t* k, const uint8_t* v, uint16_t* kd, uint16_t* vd, long long rows) {
+    const long long chunk = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (chunk >= rows * 8) return;
+    const uint8_t* src = (blockIdx.y ? v : k) + (chunk >> 3) * kQ8Row;
+    uint16_t* dst = (blockIdx.y ? vd : kd) + (chunk >> 3) * kDim;
+    const int c = (int)(chunk & 7);
+    const u32x2 c0 = *reinterpret_cast<const u32x2*>(src + 16 * c);
+    const u32x2 c1 = *reinterpret_cast<const u32x2*>(src + 16 * c + 8);
+    const uint32_t sc = *reinterpret_cast<const uint16_t*>(src + 128 + 2 * (c >> 1));
+    typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+    const half2 s2 = __builtin_bit_cast(half2, sc | (sc << 16));
+    const uint32_t cw[4] = {c0.x, c0.y, c1.x, c1.y};
+    uint32_t w[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        uint32_t lo, hi;
+        codes4_to_f16(cw[e], lo, hi);
+        w[2 * e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, lo) * s2);
+        w[2 * e + 1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, hi) * s2);
+    }
+    u32x4* out = reinterpret_cast<u32x4*>(dst + 16 * c);
+    out[0] = u32x4{w[0], w[1], w[2], w[3]};
+    out[1] = u32x4{w[4], w[5], w[6], w[7]};
 }
 
 // parts within the limits of the workspace layout and the counter slot, else 1
@@ -1614,6 +1689,30 @@ int launch_f16(const PrefillArgs& a, hipStream_t stream) {
     return check_launch("prefill_f16_kernel4");
 }
 
+// q8_0 cache, F16 precision: the rows the kernels read (ceil64(pos0 + tokens) positions) are
+// dequantised into the stream's cached f16 workspace (`workspace`) and the f16 kernels run on it: the values are those prefill_q8_kernel4 computes in registers,
+// f16(code * scale), and the f16 kernels' tile schedule is the faster one.
+template <int HW>
+int launch_q8_via_f16(const PrefillArgs& a, hipStream_t stream) {
+    const long long rows = (long long)((a.pos0 + a.tokens + 63) / 64 * 64) * a.hkv;
+    const size_t bytes = (size_t)rows * kDim * 2;
+    void* ws = nullptr;
+    const hipError_t e = workspace(kWsQ8Staging, 2 * bytes, stream, &ws);
+    if (e != hipSuccess)
+        return set_error(BRASA_ERR_LAUNCH, "flash_attention: workspace allocation (%zu bytes): %s",
+                         2 * bytes, hipGetErrorString(e));
+    uint16_t* kd = static_cast<uint16_t*>(ws);
+    uint16_t* vd = kd + rows * kDim;
+    hipLaunchKernelGGL(dequant_q8_f16_kernel, dim3((unsigned)((rows * 8 + 255) / 256), 2), dim3(256),
+                       0, stream, a.k, a.v, kd, vd, rows);
+    const int st = check_launch("dequant_q8_f16_kernel");
+    if (st != BRASA_OK) return st;
+    PrefillArgs b = a;
+    b.k = reinterpret_cast<const uint8_t*>(kd);
+    b.v = reinterpret_cast<const uint8_t*>(vd);
+    return launch_f16<HW, false>(b, stream);
+}
+
 template <int KV, int HW>
 int launch_prec(const PrefillArgs& a, int precision, hipStream_t stream) {
     if constexpr (KV == BRASA_KV_F16) {
@@ -1622,15 +1721,21 @@ int launch_prec(const PrefillArgs& a, int precision, hipStream_t stream) {
     }
     if constexpr (KV == BRASA_KV_Q8_0) {
         if (precision == BRASA_PREFILL_F16) {
-            // two workgroups per CU
-            const long long wgs = (long long)(a.hq / HW) * a.ntiles;
-            const int parts = clamp_parts(key_parts(wgs, a.pos0 + a.tokens, 512), wgs);
-            if (parts > 1)
-                return launch_split(prefill_q8_kernel4<HW>, "prefill_q8_kernel4", a, HW, wgs, parts,
-                                    kThreads, stream);
-            hipLaunchKernelGGL((prefill_q8_kernel4<HW>), dim3(a.hq / HW, a.ntiles), dim3(kThreads),
-                               0, stream, a);
-            return check_launch("prefill_q8_kernel4");
+            // the f16 kernels on dequantised rows when the work is large enough to hide the
+            // dequantisation launch (measured: T = 384 at pos0 0 is the crossover; 128 tokens
+            // after 16384 cached positions already gain 81 -> 71 us), else the q8_0 kernel
+            if ((long long)a.tokens * (a.pos0 + a.tokens) < 384LL * 384) {
+                // two workgroups per CU
+                const long long wgs = (long long)(a.hq / HW) * a.ntiles;
+                const int parts = clamp_parts(key_parts(wgs, a.pos0 + a.tokens, 512), wgs);
+                if (parts > 1)
+                    return launch_split(prefill_q8_kernel4<HW>, "prefill_q8_kernel4", a, HW, wgs,
+                                        parts, kThreads, stream);
+                hipLaunchKernelGGL((prefill_q8_kernel4<HW>), dim3(a.hq / HW, a.ntiles),
+                                   dim3(kThreads), 0, stream, a);
+                return check_launch("prefill_q8_kernel4");
+            }
+            return launch_q8_via_f16<HW>(a, stream);
         }
     }
     switch (precision) {
@@ -1653,6 +1758,25 @@ int launch_kv(PrefillArgs& a, int precision, hipStream_t stream) {
 }
 
 }  // namespace
+
+int prefill_release_workspaces() {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    hipError_t first = hipSuccess;
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    for (auto& kv : g_ws) {
+        if (!kv.second.p || e != hipSuccess) continue;
+        e = hipSetDevice(kv.first.dev);
+        if (e == hipSuccess) e = hipFree(kv.second.p);  // waits for the device's work
+        if (e != hipSuccess && first == hipSuccess) first = e;
+        e = hipSuccess;
+    }
+    if (hipSetDevice(cur) != hipSuccess && first == hipSuccess) first = hipErrorInvalidDevice;
+    g_ws.clear();
+    return first == hipSuccess ? BRASA_OK
+                               : set_error(BRASA_ERR_LAUNCH, "release_workspaces: hipFree: %s",
+                                           hipGetErrorString(first));
+}
 
 void prefill_set_layout(int variant, int pair, int parts) {
     g_force_variant.store(variant, std::memory_order_relaxed);

@@ -188,9 +188,12 @@ int brasa_decode_attention_batch(const float* q, const void* const* k, const voi
  * (BRASA_ERR_UNSUPPORTED otherwise), as the reference asserts (lib.rs:1227-1231). A launch
  * that would fill at most half of the GPU with long key ranges per query tile (a short chunk
  * after a long cached prefix, e.g. 512 tokens at pos0 16384) splits each tile's keys over up to
- * 8 workgroups; their partials go to a workspace taken with hipMallocAsync and released with
- * hipFreeAsync on `stream` (68 KB per part and query tile). The result does not depend on the
- * order in which the parts finish.
+ * 8 workgroups; their partials go to a workspace (68 KB per part and query tile). With a q8_0
+ * cache and BRASA_PREFILL_F16, the rows read (ceil64(pos0 + tokens) positions) are first
+ * dequantised to f16 (each value f16(code * scale)) into a second workspace (512 B per row of K
+ * and V), and the f16 kernels run on it. Workspaces are kept per (device, stream), grown with
+ * hipMallocAsync / hipFreeAsync on `stream` when a call needs more, and otherwise reused; see
+ * brasa_release_workspaces. The result does not depend on the order in which the parts finish.
  */
 int brasa_flash_attention_with(const float* q, const void* k, const void* v, void* o,
                                brasa_attn_shape shape, int precision, void* stream);
@@ -245,6 +248,16 @@ int brasa_rope_neox(float* x, brasa_rope_table_view table, size_t tokens, size_t
 int brasa_qk_norm_rope_store(int kv, float* q, float* k, const float* v, const float* q_norm,
                              const float* k_norm, float eps, brasa_rope_table_view table,
                              void* k_dst, void* v_dst, brasa_attn_shape shape, void* stream);
+
+/*
+ * No counterpart in the reference. Frees the prefill workspaces the library keeps, one per
+ * (device, stream) and kind: the key-split partials and the f16 staging of a q8_0 cache (see
+ * brasa_flash_attention_with). They are grown on demand and otherwise kept from call to call;
+ * this call waits for the devices' work and releases them (a later prefill call allocates
+ * again). Call it only while no prefill call is being enqueued, e.g. before destroying the
+ * streams they were used on, or at shutdown.
+ */
+int brasa_release_workspaces(void);
 
 /*
  * Test hook (no counterpart in the reference; a production caller never needs it). The prefill

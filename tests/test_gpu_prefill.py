@@ -240,8 +240,8 @@ def test_flash_key_split(parts):
 
 
 def test_flash_key_split_q8():
-    # q8_0 cache, F16 precision: 64 tokens after 8192 cached positions is 16 workgroups of the
-    # q8_0 kernel, which the launch splits into 8 key parts by itself
+    # q8_0 cache, F16 precision (the f16 kernels on the dequantised rows): 64 tokens after 8192
+    # cached positions is 16 workgroups, which the launch splits into 8 key parts by itself
     k = Kernels()
     rng = oracle.Rng(89)
     tokens, pos0, hq, hkv = 64, 8192, HQ, HKV
@@ -257,6 +257,62 @@ def test_flash_key_split_q8():
     a, r = bars(oracle.f16_to_f32(oh), ref16)
     print(f"q8_0 key split: F16 max-abs {a:.2e} max-rel {r:.2e}")
     assert a <= 2e-3 and r <= 1e-2, (a, r)
+
+
+def test_flash_key_split_q8_kernel():
+    # a launch below the dequantisation threshold stays on the q8_0 kernel: 32 tokens after
+    # 4000 cached positions is 8 workgroups, split into 2 key parts by size
+    k = Kernels()
+    rng = oracle.Rng(96)
+    tokens, pos0 = 32, 4000
+    cap = (pos0 + tokens + 63) // 64 * 64
+    q = rng.vec(tokens * HQ * DIM, 2.0)
+    cache = KvPair(KvType.Q8_0, rng.vec(cap * HKV * DIM, 2.0), rng.vec(cap * HKV * DIM, 3.0))
+    _say(f"prefill q8_0 kernel auto split F16 T={tokens} pos0={pos0}")
+    oh = run_prefill(k, q, cache, tokens, HQ, HKV, pos0, PrefillPrecision.F16)
+    assert np.array_equal(oh, run_prefill(k, q, cache, tokens, HQ, HKV, pos0,
+                                          PrefillPrecision.F16))
+    ref16, vmax = oracle.attention(q, cache.k, cache.v, tokens, HQ, HKV, DIM, pos0, q16=True)
+    a, r = bars(oracle.f16_to_f32(oh), ref16)
+    print(f"q8_0 kernel key split: F16 max-abs {a:.2e} max-rel {r:.2e}")
+    assert a <= 2e-3 and r <= 1e-2, (a, r)
+
+
+@pytest.mark.parametrize("tokens,pos0", [(384, 0), (64, 8192), (2048, 0)])
+def test_flash_q8_equals_f16_on_dequantised_rows(tokens, pos0):
+    """q8_0 F16 prefill with tokens * (pos0 + tokens) >= 384^2 dequantises the rows it reads to
+    f16(code * scale) and runs the f16 kernels: the same bits as F16 prefill over an f16 cache
+    holding those values (rounded on the host from the oracle's exact dequantisation), at the
+    threshold, a key-split chunk and T = 2048. (Smaller launches take the q8_0 kernel, checked
+    against the oracle by the other tests.)"""
+    k = Kernels()
+    rng = oracle.Rng(97)
+    lk = pos0 + tokens
+    cap = (lk + 63) // 64 * 64
+    q = rng.vec(tokens * HQ * DIM, 2.0)
+    q8 = KvPair(KvType.Q8_0, rng.vec(cap * HKV * DIM, 2.0), rng.vec(cap * HKV * DIM, 3.0))
+    f16 = KvPair(KvType.F16, oracle.round_f16(q8.k), oracle.round_f16(q8.v))
+    _say(f"prefill q8_0 vs f16 of the dequantised rows T={tokens} pos0={pos0}")
+    a = run_prefill(k, q, q8, tokens, HQ, HKV, pos0, PrefillPrecision.F16)
+    b = run_prefill(k, q, f16, tokens, HQ, HKV, pos0, PrefillPrecision.F16)
+    assert np.array_equal(a, b)
+
+
+def test_release_workspaces():
+    """The kept workspaces (q8_0 staging, key-split partials) can be released between calls:
+    the next calls allocate again and give the same bits."""
+    k = Kernels()
+    rng = oracle.Rng(98)
+    tokens, pos0 = 64, 8192
+    cap = (pos0 + tokens + 63) // 64 * 64
+    q = rng.vec(tokens * HQ * DIM, 2.0)
+    q8 = KvPair(KvType.Q8_0, rng.vec(cap * HKV * DIM, 2.0), rng.vec(cap * HKV * DIM, 3.0))
+    _say("prefill workspaces released between calls")
+    a = run_prefill(k, q, q8, tokens, HQ, HKV, pos0, PrefillPrecision.F16)
+    assert lib().brasa_release_workspaces() == 0
+    b = run_prefill(k, q, q8, tokens, HQ, HKV, pos0, PrefillPrecision.F16)
+    assert lib().brasa_release_workspaces() == 0
+    assert np.array_equal(a, b)
 
 
 def test_flash_key_split_chosen_by_size():
