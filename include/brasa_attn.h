@@ -14,8 +14,9 @@
  *   - Decode scratch (`partials`) is caller-owned, sized by brasa_decode_partials_len(). The
  *     library's own device state is its arrival counters (the in-kernel split merges of decode
  *     and of prefill's key split; each launch returns the ones it uses to zero) and the
- *     no-allocation entry point's array. The one allocation inside an entry point is prefill's
- *     key-split workspace (see brasa_flash_attention_with).
+ *     no-allocation entry point's array. Prefill keeps workspaces per (device, stream) for
+ *     its key split and for the f16 staging of a q8_0 cache, grown inside the call on its
+ *     stream when needed (see brasa_flash_attention_with, brasa_release_workspaces).
  *   - Return value: BRASA_OK (0) or a BRASA_ERR_* code; brasa_last_error() then describes it
  *     (thread-local string, valid until the next call on the same thread).
  *
