@@ -11,6 +11,8 @@
  *     (crates/metal/src/runtime.rs:255-295), is passed as the already-offset pointer.
  *   - `stream` is a hipStream_t passed as void* (NULL = the default stream). Work is enqueued,
  *     never waited for; ordering is the stream's, as the reference's one in-order command queue.
+ *     Calls that share a stream are enqueued from one host thread at a time (the prefill
+ *     workspaces of a stream are grown and reused in its order).
  *   - Decode scratch (`partials`) is caller-owned, sized by brasa_decode_partials_len(). The
  *     library's own device state is its arrival counters (the in-kernel split merges of decode
  *     and of prefill's key split; each launch returns the ones it uses to zero) and the
