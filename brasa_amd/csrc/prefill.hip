@@ -1690,8 +1690,9 @@ int launch_f16(const PrefillArgs& a, hipStream_t stream) {
 }
 
 // q8_0 cache, F16 precision: the rows the kernels read (ceil64(pos0 + tokens) positions) are
-// dequantised into the stream's cached f16 workspace (`workspace`) and the f16 kernels run on it: the values are those prefill_q8_kernel4 computes in registers,
-// f16(code * scale), and the f16 kernels' tile schedule is the faster one.
+// dequantised into the stream's cached f16 workspace (`workspace`) and the f16 kernels run on
+// it: the values are those prefill_q8_kernel4 computes in registers, f16(code * scale), and the
+// f16 kernels' tile schedule is the faster one.
 template <int HW>
 int launch_q8_via_f16(const PrefillArgs& a, hipStream_t stream) {
     const long long rows = (long long)((a.pos0 + a.tokens + 63) / 64 * 64) * a.hkv;
