@@ -49,12 +49,15 @@ SYMBOLS = {
                                            VP]),
     "brasa_flash_attention_with": (INT, [VP, VP, VP, VP, AttnShapeC, INT, VP]),
     "brasa_flash_attention": (INT, [VP, VP, VP, VP, AttnShapeC, VP]),
+    "brasa_flash_attention_workspace_len": (SZ, [AttnShapeC, INT]),
+    "brasa_flash_attention_ws": (INT, [VP, VP, VP, VP, AttnShapeC, INT, VP, SZ, VP]),
     "brasa_rope_table": (INT, [ctypes.c_double, SZ, SZ, VP, VP]),
     "brasa_rms_norm": (INT, [VP, VP, VP, SZ, SZ, ctypes.c_float, VP]),
     "brasa_rope_neox": (INT, [VP, RopeTableC, SZ, SZ, SZ, SZ, VP]),
     "brasa_qk_norm_rope_store": (INT, [INT, VP, VP, VP, VP, VP, ctypes.c_float, RopeTableC, VP,
                                        VP, AttnShapeC, VP]),
     "brasa_test_set_prefill_layout": (INT, [INT, INT, INT]),
+    "brasa_test_stream_slot": (INT, [INT, VP, ctypes.POINTER(INT)]),
     "brasa_release_workspaces": (INT, []),
     "brasa_last_error": (ctypes.c_char_p, []),
     "brasa_version": (ctypes.c_char_p, []),
@@ -76,6 +79,7 @@ SYMBOLS = {
     "brasa_rt_event_record": (INT, [VP, VP]),
     "brasa_rt_event_elapsed_ms": (INT, [ctypes.POINTER(ctypes.c_float), VP, VP]),
     "brasa_rt_event_synchronize": (INT, [VP]),
+    "brasa_rt_mem_info": (INT, [ctypes.POINTER(SZ), ctypes.POINTER(SZ)]),
     "brasa_rt_fill_normal_f32": (INT, [VP, SZ, ctypes.c_uint64, ctypes.c_float, VP]),
 }
 

@@ -32,9 +32,11 @@ int decode_batch_launch(const float* q, const void* const* k, const void* const*
                         const int* lk, int n, float* partials, void* o, int o_f16, int hq,
                         int hkv, int kv, bool per_head, hipStream_t stream);
 int prefill_launch(const float* q, const void* k, const void* v, void* o, int tokens, int hq,
-                   int hkv, int pos0, int kv, int precision, hipStream_t stream);
+                   int hkv, int pos0, int kv, int precision, bool caller_ws, void* ws,
+                   size_t ws_len, hipStream_t stream);
+size_t prefill_workspace_len(int tokens, int hq, int hkv, int pos0, int kv, int precision);
+void prefill_release_workspaces();
 void prefill_set_layout(int variant, int pair, int parts);
-int prefill_release_workspaces();
 
 namespace {
 thread_local char g_err[512] = "";
@@ -219,9 +221,8 @@ int brasa_decode_attention_batch(const float* q, const void* const* k, const voi
                                (int)hq, (int)hkv, kv, false, as_stream(stream));
 }
 
-int brasa_flash_attention_with(const float* q, const void* k, const void* v, void* o,
-                               brasa_attn_shape s, int precision, void* stream) {
-    g_err[0] = 0;
+// Shape checks of the prefill entry points (lib.rs:1203-1204, 1227-1231).
+static int prefill_check(brasa_attn_shape s, int precision) {
     if (!valid_kv(s.kv)) return set_error(BRASA_ERR_ARG, "flash_attention: invalid kv %d", s.kv);
     if (precision != BRASA_PREFILL_F16 && precision != BRASA_PREFILL_F32 &&
         precision != BRASA_PREFILL_F16_PF32)
@@ -238,10 +239,42 @@ int brasa_flash_attention_with(const float* q, const void* k, const void* v, voi
         return set_error(BRASA_ERR_UNSUPPORTED,
                          "flash_attention: without a compiled GQA group (%zu) attention is f32 only",
                          s.hq / s.hkv);
+    return BRASA_OK;
+}
+
+int brasa_flash_attention_with(const float* q, const void* k, const void* v, void* o,
+                               brasa_attn_shape s, int precision, void* stream) {
+    g_err[0] = 0;
+    const int st = prefill_check(s, precision);
+    if (st != BRASA_OK) return st;
     if (s.tokens == 0) return BRASA_OK;
     if (!q || !k || !v || !o) return set_error(BRASA_ERR_ARG, "flash_attention: null pointer");
     return prefill_launch(q, k, v, o, (int)s.tokens, (int)s.hq, (int)s.hkv, (int)s.pos0, s.kv,
-                          precision, as_stream(stream));
+                          precision, false, nullptr, 0, as_stream(stream));
+}
+
+size_t brasa_flash_attention_workspace_len(brasa_attn_shape s, int precision) {
+    g_err[0] = 0;
+    if (prefill_check(s, precision) != BRASA_OK || s.tokens == 0) return 0;
+    return prefill_workspace_len((int)s.tokens, (int)s.hq, (int)s.hkv, (int)s.pos0, s.kv,
+                                 precision);
+}
+
+int brasa_flash_attention_ws(const float* q, const void* k, const void* v, void* o,
+                             brasa_attn_shape s, int precision, void* workspace,
+                             size_t workspace_len, void* stream) {
+    g_err[0] = 0;
+    const int st = prefill_check(s, precision);
+    if (st != BRASA_OK) return st;
+    if (s.tokens == 0) return BRASA_OK;
+    if (!q || !k || !v || !o) return set_error(BRASA_ERR_ARG, "flash_attention: null pointer");
+    const size_t need = prefill_workspace_len((int)s.tokens, (int)s.hq, (int)s.hkv, (int)s.pos0,
+                                              s.kv, precision);
+    if (workspace_len < need || (need > 0 && !workspace))
+        return set_error(BRASA_ERR_SCRATCH, "flash_attention workspace too small (%zu < %zu bytes)",
+                         workspace_len, need);
+    return prefill_launch(q, k, v, o, (int)s.tokens, (int)s.hq, (int)s.hkv, (int)s.pos0, s.kv,
+                          precision, true, workspace, workspace_len, as_stream(stream));
 }
 
 int brasa_flash_attention(const float* q, const void* k, const void* v, void* o,
@@ -304,7 +337,9 @@ int brasa_qk_norm_rope_store(int kv, float* q, float* k, const float* v, const f
 
 int brasa_release_workspaces(void) {
     g_err[0] = 0;
-    return prefill_release_workspaces();
+    prefill_release_workspaces();
+    release_stream_slots();
+    return BRASA_OK;
 }
 
 int brasa_test_set_prefill_layout(int variant, int pair, int parts) {
@@ -385,6 +420,9 @@ int brasa_rt_event_elapsed_ms(float* ms, void* start, void* stop) {
 }
 int brasa_rt_event_synchronize(void* event) {
     return hip_ok(hipEventSynchronize(static_cast<hipEvent_t>(event)), "hipEventSynchronize");
+}
+int brasa_rt_mem_info(size_t* free_bytes, size_t* total_bytes) {
+    return hip_ok(hipMemGetInfo(free_bytes, total_bytes), "hipMemGetInfo");
 }
 int brasa_rt_fill_normal_f32(float* out, size_t n, uint64_t seed, float scale, void* stream) {
     return fill_normal_launch(out, n, seed, scale, as_stream(stream));

@@ -22,6 +22,15 @@ constexpr float kLog2e = 1.4426950408889634f;
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 
+// ---- per-stream slots of the library's device-side launch state (slots.hip) ----------------
+constexpr int kMaxDevices = 64;
+constexpr int kStreamSlots = 64;
+// The current device and the slot of `stream` on it (0 .. kStreamSlots - 1, the same slot for
+// every call on that stream until release_stream_slots()); slot -1 when every slot of the
+// device is taken.
+int stream_slot(hipStream_t stream, int* dev, int* slot);
+void release_stream_slots();
+
 // Decode launch plan (decode.hip): keys per split, splits of the longest sequence, and head
 // groups per workgroup.
 struct DecodePlan {

@@ -72,12 +72,11 @@ constexpr int kMaxSeqs = 64;
 // all rows packed in one line the last arrivals of a 16K-key decode waited ~2 us on each
 // other), kSlotCounters words per slot. They start at zero when the library is loaded and every
 // launch returns the counters it uses to zero (the last arrival wraps them), so nothing clears
-// them. Consecutive launches take consecutive slots: launches on different streams only share
-// counters when kCounterSlots of them are in flight at once.
+// them. Each stream has a slot of its own (stream_slot): launches on one stream run in order,
+// so no two launches in flight share counters.
 constexpr int kCtrStride = 16;
 constexpr int kSlotCounters = 16384;
-constexpr int kCounterSlots = 64;
-__device__ unsigned g_arrivals[kCounterSlots * kSlotCounters];
+__device__ unsigned g_arrivals[kStreamSlots * kSlotCounters];
 
 // Split partials of brasa_decode_attention_lanes_noalloc: one fixed array per device, used in
 // place of the caller's scratch (BRASA_DECODE_NOALLOC_FLOATS floats; a call needs
@@ -1286,25 +1285,22 @@ DecodeArgs<1> one_seq(const DecodeArgs<kMaxSeqs>& a) {
     return b;
 }
 
-// Device address of the arrival counters, looked up once per device.
-constexpr int kMaxDevices = 64;
+// This stream's arrival counters (its slot of g_arrivals; the device address looked up once per
+// device), or nullptr when every slot of the device is taken.
 unsigned* g_ctr_base[kMaxDevices];
 std::once_flag g_ctr_once[kMaxDevices];
-std::atomic<unsigned> g_next_slot{0};
 
-int arrival_counters(unsigned** out) {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return set_error(BRASA_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
-    if (dev < 0 || dev >= kMaxDevices) return set_error(BRASA_ERR_LAUNCH, "device %d out of range", dev);
+int arrival_counters(hipStream_t stream, unsigned** out) {
+    int dev = 0, slot = -1;
+    const int st = stream_slot(stream, &dev, &slot);
+    if (st != BRASA_OK) return st;
     std::call_once(g_ctr_once[dev], [dev] {
         void* p = nullptr;
         if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_arrivals)) == hipSuccess)
             g_ctr_base[dev] = static_cast<unsigned*>(p);
     });
     if (!g_ctr_base[dev]) return set_error(BRASA_ERR_LAUNCH, "decode: arrival counters not found");
-    const unsigned slot = g_next_slot.fetch_add(1, std::memory_order_relaxed) % kCounterSlots;
-    *out = g_ctr_base[dev] + (size_t)slot * kSlotCounters;
+    *out = slot < 0 ? nullptr : g_ctr_base[dev] + (size_t)slot * kSlotCounters;
     return BRASA_OK;
 }
 
@@ -1373,10 +1369,17 @@ int decode_batch_launch(const float* q, const void* const* k, const void* const*
         a.ngroups = ngroups;
         a.nseq = nb;
         a.scale = 1.0f / sqrtf(static_cast<float>(kDim));
-        int st = arrival_counters(&a.ctr);
+        int st = arrival_counters(stream, &a.ctr);
         if (st != BRASA_OK) return st;
-        // one split length for the launch (a sequence's splits never exceed ceil(lk / 128))
-        const DecodePlan plan = decode_plan(lk + b0, nb, ngroups, G, kv);
+        // one split length for the launch (a sequence's splits never exceed ceil(lk / 128));
+        // with no counter slot free (more streams than slots), one split per sequence, which
+        // needs no merge
+        DecodePlan plan = decode_plan(lk + b0, nb, ngroups, G, kv);
+        if (!a.ctr) {
+            int lmax = 1;
+            for (int i = 0; i < nb; ++i) lmax = std::max(lmax, lk[b0 + i]);
+            plan = DecodePlan{(lmax + kBlock - 1) / kBlock * kBlock, 1, plan.hpw};
+        }
         const long long chunk = plan.chunk;
         int col = 0;
         for (int i = 0; i < nb; ++i) {
@@ -1390,6 +1393,11 @@ int decode_batch_launch(const float* q, const void* const* k, const void* const*
             d.split0 = col;
             d.part_off = part_off;
             col += d.splits;
+            // every plan keeps a sequence's partials inside its share of the scratch
+            // (brasa_decode_partials_len of its length)
+            if (d.splits > (int)((lk[b0 + i] + kMinChunk - 1) / kMinChunk))
+                return set_error(BRASA_ERR_SCRATCH, "decode: %d splits exceed the scratch of %d keys",
+                                 d.splits, lk[b0 + i]);
             part_off += (size_t)hq * d.splits * (kDim + 2);
         }
         st = nb == 1 ? launch_kv(one_seq(a), kv, G, plan.hpw, col, stream)

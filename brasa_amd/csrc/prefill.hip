@@ -27,7 +27,6 @@
 //     phases alternate; up to two workgroups per CU), prefill_f16_kernel4 (4 waves, two per CU)
 //     and prefill_f16_kernel4s (4 waves on 32-key stages, three per CU).
 #include <atomic>
-#include <map>
 #include <mutex>
 #include <type_traits>
 
@@ -60,7 +59,22 @@ struct PrefillArgs {
     int kparts;
     float* part;
     unsigned* ctr;
+    // q8_0 caches in F16 precision, whose values go through f16(code * scale): a launch that
+    // meets a scale outside the range where that product is a normal f16 (see q8_f16_unsafe)
+    // stores `tag` at `taint`; the exact kernel launched after it runs only when *gate == tag
+    unsigned* taint;
+    const unsigned* gate;
+    unsigned tag;
 };
+
+// True for the f16 scale bits of a q8_0 group whose f16(code * scale) products can leave the
+// normal f16 range: |scale| >= 516 (127 * 516 > 65504 rounds to inf), f16-subnormal scales (the
+// products of small codes are subnormal, with fewer significant bits), and inf / NaN. Scales of
+// 0 (an all-zero group) are exact.
+__device__ __forceinline__ bool q8_f16_unsafe(uint32_t sc) {
+    const uint32_t m = sc & 0x7fffu;
+    return m >= 0x6008u || (m != 0 && m < 0x0400u);
+}
 
 
 #ifdef BRASA_PREFILL_TRACE
@@ -234,6 +248,7 @@ __device__ __forceinline__ void q_convert_half(const u32x4 (&raw)[8], float scal
 template <int KV, int HW, bool QS, bool PS, bool OF32>
 __global__ void __launch_bounds__(kThreads, 2)
 prefill_kernel(PrefillArgs a) {
+    if (a.gate && *a.gate != a.tag) return;  // the fast launch before this one was exact
     constexpr bool KS = (KV != BRASA_KV_F16);  // cache values need hi/lo
     constexpr int NK = KS ? 2 : 1;
     constexpr int TPW = 32 * 4 / HW;            // query tokens per workgroup
@@ -1195,12 +1210,14 @@ prefill_q8_kernel4(PrefillArgs a) {
             w[2 * e + 1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, hi) * s2);
         }
     };
+    bool unsafe = false;  // a scale outside q8_f16_unsafe's range was met
     auto store_rows = [&](const Q8Rows& q, int buf) {
         uint8_t* kt = reinterpret_cast<uint8_t*>(&s_k[buf][0]);
         uint8_t* vt = reinterpret_cast<uint8_t*>(&s_vv[buf][0]);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int row = 16 * wave + rr + 8 * i;
+            unsafe = unsafe || q8_f16_unsafe(q.ks[i]) || q8_f16_unsafe(q.vs[i]);
             uint32_t w[8];
             deq(q.kc[i], q.ks[i], w);
 #pragma unroll
@@ -1316,6 +1333,7 @@ prefill_q8_kernel4(PrefillArgs a) {
     }
 
     __syncthreads();  // every wave is done with the K stages: wave w stages its output in 8 KB of them
+    if (a.taint && __builtin_amdgcn_ballot_w64(unsafe) != 0 && lane == 0) *a.taint = a.tag;
     if (a.kparts > 1 && !merge_key_parts(a, tile, part, wave, lane, acc, m_used, lsum)) return;
     const float L = sum_xor32(lsum);
     const float inv = 1.0f / L;
@@ -1505,13 +1523,6 @@ prefill_f16_kernel4s(PrefillArgs a) {
                  a.o, tw0, a.tokens, a.hq, h);
 }
 
-template <int KV, int HW, bool QS, bool PS, bool OF32>
-int launch(const PrefillArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL((prefill_kernel<KV, HW, QS, PS, OF32>), dim3(a.hq / HW, a.ntiles),
-                       dim3(kThreads), 0, stream, a);
-    return check_launch("prefill_kernel");
-}
-
 // Kernel choice by workgroup count (one per query tile and head group), measured on one box at
 // hq 32 / hkv 8: up to two per CU the two-group kernel, which splits each tile's keys over two
 // wave groups (T = 2048: 512 workgroups, 58 vs 63 µs for the others; T = 512 at pos0 16384: 128
@@ -1526,64 +1537,56 @@ std::atomic<int> g_allow_pair{1};
 std::atomic<int> g_force_parts{1};    // key parts of a forced prefill_f16_kernel launch
 
 
-// Arrival counters of the key-split merge: one per (query tile, wave), 64 bytes apart, in
-// kPfCounterSlots slots taken round robin per launch; zero at load, returned to zero by every
-// launch (the last arrival wraps them).
+// Arrival counters of the key-split merge: one per (query tile, wave), 64 bytes apart; a slot
+// of kPfSlotWords per stream (stream_slot), zero at load, returned to zero by every launch (the
+// last arrival wraps them). Next to them, one word per stream for the q8_0 range flag.
 constexpr int kPfSlotWords = 16384;
-constexpr int kPfCounterSlots = 64;
-__device__ unsigned g_pf_arrivals[kPfCounterSlots * kPfSlotWords];
-std::atomic<unsigned> g_pf_next_slot{0};
-unsigned* g_pf_ctr_base[64];
-std::once_flag g_pf_ctr_once[64];
+__device__ unsigned g_pf_arrivals[kStreamSlots * kPfSlotWords];
+__device__ unsigned g_pf_taint[kStreamSlots * 16];
+unsigned* g_pf_ctr_base[kMaxDevices];
+unsigned* g_pf_taint_base[kMaxDevices];
+std::once_flag g_pf_ctr_once[kMaxDevices];
+// Launch tags of the q8_0 range flag: one per call, never 0.
+std::atomic<unsigned> g_pf_tag{0};
 
-// Workspaces (key-split partials, q8_0 staging): one cached buffer per (device, stream, kind),
-// grown with hipMallocAsync / hipFreeAsync on that stream when a call needs more and otherwise
-// reused as it is. Calls on one stream run in order, so a stream's buffer is never used by two
-// launches at once; calls on different streams get different buffers. (An allocation and a
-// free per call cost ~5.7 us of idle GPU between launches, from the default pool and from a
-// pool that keeps its memory alike.) Held until brasa_release_workspaces() or process exit.
-enum WsKind { kWsKeySplit = 0, kWsQ8Staging = 1 };
-struct WsKey {
-    int dev;
-    hipStream_t stream;
-    int kind;
-    bool operator<(const WsKey& o) const {
-        if (dev != o.dev) return dev < o.dev;
-        if (stream != o.stream) return stream < o.stream;
-        return kind < o.kind;
+// The workspace of the reference-signature entry points (brasa_flash_attention[_with]), which
+// take none: a fixed device array, so those calls allocate nothing. One stream per device owns
+// it (the first to need it, until brasa_release_workspaces()); calls on other streams, and calls
+// whose plan needs more, use the plans that fit (no key split, no q8_0 staging: slower, same
+// results up to the split's last-bit effects). Sized for a q8_0 chunk of 512 tokens after 16384
+// cached positions with its key split (69 MB of staging, 17 MB of partials).
+constexpr size_t kStaticWsBytes = (size_t)96 << 20;
+__device__ __align__(256) uint8_t g_pf_static_ws[kStaticWsBytes];
+uint8_t* g_pf_static_base[kMaxDevices];
+std::once_flag g_pf_static_once[kMaxDevices];
+std::atomic<int> g_pf_static_owner[kMaxDevices];  // 0: free, slot + 1: owner
+
+// One call's resources: its workspace (carved front to back), the stream's counters and flag.
+// measure: nothing is launched; `need` sums what a workspace big enough for every feature of the
+// plan would hold (brasa_flash_attention_workspace_len).
+struct PfCtx {
+    hipStream_t stream = nullptr;
+    uint8_t* ws = nullptr;
+    size_t ws_len = 0;
+    size_t used = 0;
+    bool measure = false;
+    size_t need = 0;
+    unsigned* ctr = nullptr;
+    unsigned* taint = nullptr;
+    unsigned tag = 0;
+
+    void* take(size_t bytes) {
+        bytes = (bytes + 255) / 256 * 256;
+        if (measure) {
+            need += bytes;
+            return reinterpret_cast<void*>(static_cast<uintptr_t>(256));  // never dereferenced
+        }
+        if (!ws || used + bytes > ws_len) return nullptr;
+        void* p = ws + used;
+        used += bytes;
+        return p;
     }
 };
-struct WsBuf {
-    void* p = nullptr;
-    size_t bytes = 0;
-};
-std::mutex g_ws_mu;
-std::map<WsKey, WsBuf> g_ws;
-
-hipError_t workspace(WsKind kind, size_t bytes, hipStream_t stream, void** out) {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
-    std::lock_guard<std::mutex> lock(g_ws_mu);
-    WsBuf& b = g_ws[WsKey{dev, stream, kind}];
-    if (b.bytes < bytes) {
-        const size_t grow = (bytes + (2u << 20) - 1) / (2u << 20) * (2u << 20);  // 2 MiB steps
-        if (b.p) {
-            e = hipFreeAsync(b.p, stream);
-            b.p = nullptr;
-            b.bytes = 0;
-            if (e != hipSuccess) return e;
-        }
-        e = hipMallocAsync(&b.p, grow, stream);
-        if (e != hipSuccess) {
-            b.p = nullptr;
-            return e;
-        }
-        b.bytes = grow;
-    }
-    *out = b.p;
-    return hipSuccess;
-}
 
 // Key parts per query tile: 1 (no split) unless the launch fills at most half of the
 // workgroup slots (`slots`: CUs x workgroups per CU of the kernel) and the tiles' keys are long
@@ -1595,42 +1598,35 @@ int key_parts(long long wgs, int keys, int slots) {
     return parts;
 }
 
-// Launches `kernel` over (hq / HW) x (rows * parts) workgroups with a key split of `parts`:
-// the arrival counters of the launch (a slot of g_pf_arrivals) and a stream-ordered workspace
-// for the parts' partials, freed on the same stream after the kernel.
+// parts within the limits of the workspace layout and the counter slot, else 1
+int clamp_parts(int parts, long long wgs) {
+    return (parts < 1 || parts > kMaxKeyParts || wgs * 4 * 16 > kPfSlotWords) ? 1 : parts;
+}
+
+// Launches `kernel` over (hq / HW) x (rows * parts) workgroups with a key split of `parts`
+// (the stream's arrival counters, the parts' partials in the call's workspace). Returns 1 when
+// the workspace or the counters are missing: the caller then launches unsplit.
 template <typename K>
-int launch_split(K kernel, const char* name, PrefillArgs b, int hw, long long wgs, int parts,
-                 int threads, hipStream_t stream) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
-        return set_error(BRASA_ERR_LAUNCH, "flash_attention: no device");
-    std::call_once(g_pf_ctr_once[dev], [dev] {
-        void* p = nullptr;
-        if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_pf_arrivals)) == hipSuccess)
-            g_pf_ctr_base[dev] = static_cast<unsigned*>(p);
-    });
-    if (!g_pf_ctr_base[dev])
-        return set_error(BRASA_ERR_LAUNCH, "flash_attention: arrival counters not found");
-    const unsigned slot = g_pf_next_slot.fetch_add(1, std::memory_order_relaxed) % kPfCounterSlots;
-    void* ws = nullptr;
-    const size_t bytes = (size_t)wgs * parts * kKeyPartFloats * sizeof(float);
-    hipError_t e = workspace(kWsKeySplit, bytes, stream, &ws);
-    if (e != hipSuccess)
-        return set_error(BRASA_ERR_LAUNCH, "flash_attention: workspace allocation (%zu bytes): %s",
-                         bytes, hipGetErrorString(e));
+int launch_split(PfCtx& c, K kernel, const char* name, PrefillArgs b, int hw, long long wgs,
+                 int parts, int threads) {
+    void* ws = c.take((size_t)wgs * parts * kKeyPartFloats * sizeof(float));
+    if (!ws || !c.ctr) return 1;
+    if (c.measure) return BRASA_OK;
     b.pair = 0;
     b.kparts = parts;
     b.part = static_cast<float*>(ws);
-    b.ctr = g_pf_ctr_base[dev] + (size_t)slot * kPfSlotWords;
-    hipLaunchKernelGGL(kernel, dim3(b.hq / hw, b.ntiles * parts), dim3(threads), 0, stream, b);
+    b.ctr = c.ctr;
+    hipLaunchKernelGGL(kernel, dim3(b.hq / hw, b.ntiles * parts), dim3(threads), 0, c.stream, b);
     return check_launch(name);
 }
 
 // q8_0 rows -> f16 rows [rows, 128], each value f16(code * scale) by the same packed f16 multiply
 // as prefill_q8_kernel4 (bit-identical values). One thread per 16-code chunk (two 8-byte code
-// loads and the chunk's scale; 136-byte rows are 8-byte aligned); grid y: K, V.
+// loads and the chunk's scale; 136-byte rows are 8-byte aligned); grid y: K, V. A scale for
+// which those values can leave the normal f16 range stores `tag` at `taint`.
 __global__ void __launch_bounds__(256)
-dequant_q8_f16_kernel(const uint8_t* k, const uint8_t* v, uint16_t* kd, uint16_t* vd, long long rows) {
+dequant_q8_f16_kernel(const uint8_t* k, const uint8_t* v, uint16_t* kd, uint16_t* vd,
+                      long long rows, unsigned* taint, unsigned tag) {
     const long long chunk = (long long)blockIdx.x * 256 + threadIdx.x;
     if (chunk >= rows * 8) return;
     const uint8_t* src = (blockIdx.y ? v : k) + (chunk >> 3) * kQ8Row;
@@ -1639,6 +1635,7 @@ dequant_q8_f16_kernel(const uint8_t* k, const uint8_t* v, uint16_t* kd, uint16_t
     const u32x2 c0 = *reinterpret_cast<const u32x2*>(src + 16 * c);
     const u32x2 c1 = *reinterpret_cast<const u32x2*>(src + 16 * c + 8);
     const uint32_t sc = *reinterpret_cast<const uint16_t*>(src + 128 + 2 * (c >> 1));
+    if (q8_f16_unsafe(sc)) *taint = tag;
     typedef _Float16 half2 __attribute__((ext_vector_type(2)));
     const half2 s2 = __builtin_bit_cast(half2, sc | (sc << 16));
     const uint32_t cw[4] = {c0.x, c0.y, c1.x, c1.y};
@@ -1655,13 +1652,81 @@ dequant_q8_f16_kernel(const uint8_t* k, const uint8_t* v, uint16_t* kd, uint16_t
     out[1] = u32x4{w[4], w[5], w[6], w[7]};
 }
 
-// parts within the limits of the workspace layout and the counter slot, else 1
-int clamp_parts(int parts, long long wgs) {
-    return (parts < 1 || parts > kMaxKeyParts || wgs * 4 * 16 > kPfSlotWords) ? 1 : parts;
+// Two values d, d + 1 (d even) of cache row `row` as f32 (q8_0: code * scale, exact).
+template <int KV>
+__device__ __forceinline__ f32x2 row_pair(const uint8_t* cache, size_t row, int d) {
+    if constexpr (KV == BRASA_KV_F32) {
+        return *reinterpret_cast<const f32x2*>(cache + row * 512 + 4 * d);
+    } else if constexpr (KV == BRASA_KV_F16) {
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(cache + row * 256 + 2 * d);
+        return f32x2{h2f((uint16_t)(w & 0xffffu)), h2f((uint16_t)(w >> 16))};
+    } else {
+        const uint8_t* r = cache + row * kQ8Row;
+        const uint16_t c = *reinterpret_cast<const uint16_t*>(r + d);
+        const float sc = h2f(*reinterpret_cast<const uint16_t*>(r + 128 + 2 * (d >> 5)));
+        return f32x2{(float)(int8_t)(c & 0xffu) * sc, (float)(int8_t)(c >> 8) * sc};
+    }
+}
+
+// Exact F16 prefill in plain f32 arithmetic, the reference F16 kernel's numerics
+// (flash_attention.metal:152-323: Q * scale rounded to f16, K / V as exact f32 values, scores,
+// softmax, P and O in f32, o rounded to f16). One wave per (query token, query head), lane l
+// holding dims 2 l, 2 l + 1; one key per step (the score is a wave sum). Slow, and free of any
+// f16 range limit on the cache values: the recompute of q8_0 calls whose f16(code * scale)
+// values leave the normal f16 range (it runs only when *gate == tag, i.e. after the fast launch
+// flagged such a scale; otherwise every wave exits at once).
+template <int KV>
+__global__ void __launch_bounds__(256)
+prefill_exact_kernel(PrefillArgs a) {
+    if (a.gate && *a.gate != a.tag) return;
+    const int lane = threadIdx.x & 63;
+    const int rw = blockIdx.x * 4 + (threadIdx.x >> 6);  // query token * hq + query head
+    if (rw >= a.tokens * a.hq) return;
+    const int t = rw / a.hq, h = rw - t * a.hq, kh = h / a.group, d = 2 * lane;
+    const f32x2 qv = *reinterpret_cast<const f32x2*>(a.q + (size_t)rw * kDim + d);
+    const float q0 = h2f(f2h(as_f32(qv.x * a.scale))), q1 = h2f(f2h(as_f32(qv.y * a.scale)));
+    float m = -INFINITY, l = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    const int kend = a.pos0 + t + 1;
+    for (int j = 0; j < kend; ++j) {
+        const size_t row = (size_t)j * a.hkv + kh;
+        const f32x2 kk = row_pair<KV>(a.k, row, d);
+        const f32x2 vv = row_pair<KV>(a.v, row, d);
+        float sc = row16_sum(fmaf(q0, kk.x, q1 * kk.y));
+        sc += __shfl_xor(sc, 16, 64);
+        sc += __shfl_xor(sc, 32, 64);
+        const float x = sc * kLog2e;
+        const float mn = fmaxf(m, x);
+        const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+        const float p = __builtin_amdgcn_exp2f(x - mn);
+        l = fmaf(l, alpha, p);
+        o0 = fmaf(o0, alpha, p * vv.x);
+        o1 = fmaf(o1, alpha, p * vv.y);
+        m = mn;
+    }
+    const float inv = 1.0f / l;
+    *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.o) + (size_t)rw * kDim + d) =
+        (uint32_t)f2h(o0 * inv) | ((uint32_t)f2h(o1 * inv) << 16);
+}
+
+template <int KV>
+int launch_exact(PfCtx& c, const PrefillArgs& a) {
+    if (c.measure) return BRASA_OK;
+    const long long rows = (long long)a.tokens * a.hq;
+    hipLaunchKernelGGL(prefill_exact_kernel<KV>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                       c.stream, a);
+    return check_launch("prefill_exact_kernel");
+}
+
+template <int KV, int HW, bool QS, bool PS, bool OF32>
+int launch(PfCtx& c, const PrefillArgs& a) {
+    if (c.measure) return BRASA_OK;
+    hipLaunchKernelGGL((prefill_kernel<KV, HW, QS, PS, OF32>), dim3(a.hq / HW, a.ntiles),
+                       dim3(kThreads), 0, c.stream, a);
+    return check_launch("prefill_kernel");
 }
 
 template <int HW, bool PS>
-int launch_f16(const PrefillArgs& a, hipStream_t stream) {
+int launch_f16(PfCtx& c, const PrefillArgs& a) {
     const long long wgs = (long long)(a.hq / HW) * a.ntiles;
     const int variant = g_force_variant.load(std::memory_order_relaxed);
     const int pick = variant ? variant : wgs <= 2 * 256 ? 1 : wgs < 3 * 256 ? 2 : 4;
@@ -1671,122 +1736,118 @@ int launch_f16(const PrefillArgs& a, hipStream_t stream) {
         // one workgroup per CU
         const int parts = clamp_parts(variant ? g_force_parts.load(std::memory_order_relaxed)
                                               : key_parts(wgs, a.pos0 + a.tokens, 256), wgs);
-        if (parts > 1)
-            return launch_split(prefill_f16_kernel<HW, PS>, "prefill_f16_kernel", b, HW, wgs, parts,
-                                2 * kThreads, stream);
+        if (parts > 1) {
+            const int st = launch_split(c, prefill_f16_kernel<HW, PS>, "prefill_f16_kernel", b, HW,
+                                        wgs, parts, 2 * kThreads);
+            if (st != 1) return st;
+        }
+        if (c.measure) return BRASA_OK;
         const int rows = b.pair ? (a.ntiles + 1) / 2 : a.ntiles;
         hipLaunchKernelGGL((prefill_f16_kernel<HW, PS>), dim3(a.hq / HW, rows),
-                           dim3(2 * kThreads), 0, stream, b);
+                           dim3(2 * kThreads), 0, c.stream, b);
         return check_launch("prefill_f16_kernel");
     }
+    if (c.measure) return BRASA_OK;
     if (pick == 4) {
         hipLaunchKernelGGL((prefill_f16_kernel4s<HW, PS>), dim3(a.hq / HW, a.ntiles), dim3(kThreads),
-                           0, stream, a);
+                           0, c.stream, a);
         return check_launch("prefill_f16_kernel4s");
     }
     hipLaunchKernelGGL((prefill_f16_kernel4<HW, PS>), dim3(a.hq / HW, a.ntiles), dim3(kThreads), 0,
-                       stream, a);
+                       c.stream, a);
     return check_launch("prefill_f16_kernel4");
 }
 
-// q8_0 cache, F16 precision: the rows the kernels read (ceil64(pos0 + tokens) positions) are
-// dequantised into the stream's cached f16 workspace (`workspace`) and the f16 kernels run on
-// it: the values are those prefill_q8_kernel4 computes in registers, f16(code * scale), and the
-// f16 kernels' tile schedule is the faster one.
+// q8_0 cache, F16 precision, small launches: prefill_q8_kernel4 (f16(code * scale) in registers)
 template <int HW>
-int launch_q8_via_f16(const PrefillArgs& a, hipStream_t stream) {
+int launch_q8_kernel4(PfCtx& c, const PrefillArgs& a) {
+    // two workgroups per CU
+    const long long wgs = (long long)(a.hq / HW) * a.ntiles;
+    const int parts = clamp_parts(key_parts(wgs, a.pos0 + a.tokens, 512), wgs);
+    if (parts > 1) {
+        const int st = launch_split(c, prefill_q8_kernel4<HW>, "prefill_q8_kernel4", a, HW, wgs,
+                                    parts, kThreads);
+        if (st != 1) return st;
+    }
+    if (c.measure) return BRASA_OK;
+    hipLaunchKernelGGL((prefill_q8_kernel4<HW>), dim3(a.hq / HW, a.ntiles), dim3(kThreads), 0,
+                       c.stream, a);
+    return check_launch("prefill_q8_kernel4");
+}
+
+// q8_0 cache, F16 precision, large launches: the rows the kernels read (ceil64(pos0 + tokens)
+// positions) are dequantised into the call's workspace and the f16 kernels run on them: the
+// values are those prefill_q8_kernel4 computes in registers, f16(code * scale), and the f16
+// kernels' tile schedule is the faster one. Without room for the staging: prefill_q8_kernel4.
+template <int HW>
+int launch_q8_via_f16(PfCtx& c, const PrefillArgs& a) {
     const long long rows = (long long)((a.pos0 + a.tokens + 63) / 64 * 64) * a.hkv;
     const size_t bytes = (size_t)rows * kDim * 2;
-    void* ws = nullptr;
-    const hipError_t e = workspace(kWsQ8Staging, 2 * bytes, stream, &ws);
-    if (e != hipSuccess)
-        return set_error(BRASA_ERR_LAUNCH, "flash_attention: workspace allocation (%zu bytes): %s",
-                         2 * bytes, hipGetErrorString(e));
+    void* ws = c.take(2 * bytes);
+    if (!ws) return launch_q8_kernel4<HW>(c, a);
     uint16_t* kd = static_cast<uint16_t*>(ws);
     uint16_t* vd = kd + rows * kDim;
-    hipLaunchKernelGGL(dequant_q8_f16_kernel, dim3((unsigned)((rows * 8 + 255) / 256), 2), dim3(256),
-                       0, stream, a.k, a.v, kd, vd, rows);
-    const int st = check_launch("dequant_q8_f16_kernel");
-    if (st != BRASA_OK) return st;
+    if (!c.measure) {
+        hipLaunchKernelGGL(dequant_q8_f16_kernel, dim3((unsigned)((rows * 8 + 255) / 256), 2),
+                           dim3(256), 0, c.stream, a.k, a.v, kd, vd, rows, a.taint, a.tag);
+        const int st = check_launch("dequant_q8_f16_kernel");
+        if (st != BRASA_OK) return st;
+    }
     PrefillArgs b = a;
     b.k = reinterpret_cast<const uint8_t*>(kd);
     b.v = reinterpret_cast<const uint8_t*>(vd);
-    return launch_f16<HW, false>(b, stream);
+    return launch_f16<HW, false>(c, b);
 }
 
 template <int KV, int HW>
-int launch_prec(const PrefillArgs& a, int precision, hipStream_t stream) {
+int launch_prec(PfCtx& c, PrefillArgs& a, int precision) {
     if constexpr (KV == BRASA_KV_F16) {
-        if (precision == BRASA_PREFILL_F16) return launch_f16<HW, false>(a, stream);
-        if (precision == BRASA_PREFILL_F16_PF32) return launch_f16<HW, true>(a, stream);
+        if (precision == BRASA_PREFILL_F16) return launch_f16<HW, false>(c, a);
+        if (precision == BRASA_PREFILL_F16_PF32) return launch_f16<HW, true>(c, a);
     }
     if constexpr (KV == BRASA_KV_Q8_0) {
-        if (precision == BRASA_PREFILL_F16) {
+        if (precision == BRASA_PREFILL_F16 && c.taint) {
             // the f16 kernels on dequantised rows when the work is large enough to hide the
             // dequantisation launch (measured: T = 384 at pos0 0 is the crossover; 128 tokens
-            // after 16384 cached positions already gain 81 -> 71 us), else the q8_0 kernel
-            if ((long long)a.tokens * (a.pos0 + a.tokens) < 384LL * 384) {
-                // two workgroups per CU
-                const long long wgs = (long long)(a.hq / HW) * a.ntiles;
-                const int parts = clamp_parts(key_parts(wgs, a.pos0 + a.tokens, 512), wgs);
-                if (parts > 1)
-                    return launch_split(prefill_q8_kernel4<HW>, "prefill_q8_kernel4", a, HW, wgs,
-                                        parts, kThreads, stream);
-                hipLaunchKernelGGL((prefill_q8_kernel4<HW>), dim3(a.hq / HW, a.ntiles),
-                                   dim3(kThreads), 0, stream, a);
-                return check_launch("prefill_q8_kernel4");
-            }
-            return launch_q8_via_f16<HW>(a, stream);
+            // after 16384 cached positions already gain 81 -> 71 us), else the q8_0 kernel.
+            // Both flag scales whose f16(code * scale) can leave the normal f16 range; the exact
+            // kernel (the reference's F16 numerics in f32) then recomputes the call, and
+            // otherwise exits at once.
+            a.taint = c.taint;
+            a.tag = c.tag;
+            const int st = (long long)a.tokens * (a.pos0 + a.tokens) < 384LL * 384
+                               ? launch_q8_kernel4<HW>(c, a)
+                               : launch_q8_via_f16<HW>(c, a);
+            if (st != BRASA_OK) return st;
+            PrefillArgs g = a;
+            g.taint = nullptr;
+            g.gate = c.taint;
+            return launch_exact<KV>(c, g);
         }
+        // (no range flag for this stream: the exact kernel directly)
+        if (precision == BRASA_PREFILL_F16) return launch_exact<KV>(c, a);
     }
     switch (precision) {
-        case BRASA_PREFILL_F32: return launch<KV, HW, true, true, true>(a, stream);
-        case BRASA_PREFILL_F16_PF32: return launch<KV, HW, false, true, false>(a, stream);
-        default: return launch<KV, HW, false, false, false>(a, stream);
+        case BRASA_PREFILL_F32: return launch<KV, HW, true, true, true>(c, a);
+        case BRASA_PREFILL_F16_PF32: return launch<KV, HW, false, true, false>(c, a);
+        default: return launch<KV, HW, false, false, false>(c, a);
     }
 }
 
 template <int KV>
-int launch_kv(PrefillArgs& a, int precision, hipStream_t stream) {
+int launch_kv(PfCtx& c, PrefillArgs& a, int precision) {
     const int HW = (a.group % 4 == 0) ? 4 : (a.group % 2 == 0) ? 2 : 1;
     const int tpw = 32 * 4 / HW;
     a.ntiles = (a.tokens + tpw - 1) / tpw;
     switch (HW) {
-        case 4: return launch_prec<KV, 4>(a, precision, stream);
-        case 2: return launch_prec<KV, 2>(a, precision, stream);
-        default: return launch_prec<KV, 1>(a, precision, stream);
+        case 4: return launch_prec<KV, 4>(c, a, precision);
+        case 2: return launch_prec<KV, 2>(c, a, precision);
+        default: return launch_prec<KV, 1>(c, a, precision);
     }
 }
 
-}  // namespace
-
-int prefill_release_workspaces() {
-    std::lock_guard<std::mutex> lock(g_ws_mu);
-    hipError_t first = hipSuccess;
-    int cur = 0;
-    hipError_t e = hipGetDevice(&cur);
-    for (auto& kv : g_ws) {
-        if (!kv.second.p || e != hipSuccess) continue;
-        e = hipSetDevice(kv.first.dev);
-        if (e == hipSuccess) e = hipFree(kv.second.p);  // waits for the device's work
-        if (e != hipSuccess && first == hipSuccess) first = e;
-        e = hipSuccess;
-    }
-    if (hipSetDevice(cur) != hipSuccess && first == hipSuccess) first = hipErrorInvalidDevice;
-    g_ws.clear();
-    return first == hipSuccess ? BRASA_OK
-                               : set_error(BRASA_ERR_LAUNCH, "release_workspaces: hipFree: %s",
-                                           hipGetErrorString(first));
-}
-
-void prefill_set_layout(int variant, int pair, int parts) {
-    g_force_variant.store(variant, std::memory_order_relaxed);
-    g_allow_pair.store(pair, std::memory_order_relaxed);
-    g_force_parts.store(parts, std::memory_order_relaxed);
-}
-
-int prefill_launch(const float* q, const void* k, const void* v, void* o, int tokens, int hq,
-                   int hkv, int pos0, int kv, int precision, hipStream_t stream) {
+PrefillArgs make_args(const float* q, const void* k, const void* v, void* o, int tokens, int hq,
+                      int hkv, int pos0) {
     PrefillArgs a;
     a.q = q;
     a.k = static_cast<const uint8_t*>(k);
@@ -1802,13 +1863,87 @@ int prefill_launch(const float* q, const void* k, const void* v, void* o, int to
     a.kparts = 1;
     a.part = nullptr;
     a.ctr = nullptr;
+    a.taint = nullptr;
+    a.gate = nullptr;
+    a.tag = 0;
     a.scale = 1.0f / sqrtf(static_cast<float>(kDim));
+    return a;
+}
+
+int run(PfCtx& c, PrefillArgs& a, int kv, int precision) {
     switch (kv) {
-        case BRASA_KV_F32: return launch_kv<BRASA_KV_F32>(a, precision, stream);
-        case BRASA_KV_F16: return launch_kv<BRASA_KV_F16>(a, precision, stream);
-        case BRASA_KV_Q8_0: return launch_kv<BRASA_KV_Q8_0>(a, precision, stream);
+        case BRASA_KV_F32: return launch_kv<BRASA_KV_F32>(c, a, precision);
+        case BRASA_KV_F16: return launch_kv<BRASA_KV_F16>(c, a, precision);
+        case BRASA_KV_Q8_0: return launch_kv<BRASA_KV_Q8_0>(c, a, precision);
     }
     return set_error(BRASA_ERR_ARG, "flash_attention: invalid kv type %d", kv);
+}
+
+}  // namespace
+
+void prefill_release_workspaces() {
+    for (auto& o : g_pf_static_owner) o.store(0, std::memory_order_relaxed);
+}
+
+void prefill_set_layout(int variant, int pair, int parts) {
+    g_force_variant.store(variant, std::memory_order_relaxed);
+    g_allow_pair.store(pair, std::memory_order_relaxed);
+    g_force_parts.store(parts, std::memory_order_relaxed);
+}
+
+size_t prefill_workspace_len(int tokens, int hq, int hkv, int pos0, int kv, int precision) {
+    PrefillArgs a = make_args(nullptr, nullptr, nullptr, nullptr, tokens, hq, hkv, pos0);
+    PfCtx c;
+    c.measure = true;
+    c.ctr = c.taint = reinterpret_cast<unsigned*>(static_cast<uintptr_t>(256));  // never used
+    run(c, a, kv, precision);
+    return c.need;
+}
+
+// caller_ws: the caller's workspace of ws_len bytes, at least prefill_workspace_len(); otherwise
+// the reference-signature call (the fixed workspace when this stream owns it).
+int prefill_launch(const float* q, const void* k, const void* v, void* o, int tokens, int hq,
+                   int hkv, int pos0, int kv, int precision, bool caller_ws, void* ws,
+                   size_t ws_len, hipStream_t stream) {
+    int dev = 0, slot = -1;
+    int st = stream_slot(stream, &dev, &slot);
+    if (st != BRASA_OK) return st;
+    std::call_once(g_pf_ctr_once[dev], [dev] {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_pf_arrivals)) == hipSuccess)
+            g_pf_ctr_base[dev] = static_cast<unsigned*>(p);
+        p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_pf_taint)) == hipSuccess)
+            g_pf_taint_base[dev] = static_cast<unsigned*>(p);
+    });
+    if (!g_pf_ctr_base[dev] || !g_pf_taint_base[dev])
+        return set_error(BRASA_ERR_LAUNCH, "flash_attention: arrival counters not found");
+    PfCtx c;
+    c.stream = stream;
+    if (slot >= 0) {
+        c.ctr = g_pf_ctr_base[dev] + (size_t)slot * kPfSlotWords;
+        c.taint = g_pf_taint_base[dev] + (size_t)slot * 16;
+        unsigned t = 0;
+        while (t == 0) t = g_pf_tag.fetch_add(1, std::memory_order_relaxed) + 1;
+        c.tag = t;
+    }
+    if (caller_ws) {
+        c.ws = static_cast<uint8_t*>(ws);
+        c.ws_len = ws ? ws_len : 0;
+    } else if (slot >= 0) {
+        int expect = 0;
+        if (g_pf_static_owner[dev].compare_exchange_strong(expect, slot + 1) || expect == slot + 1) {
+            std::call_once(g_pf_static_once[dev], [dev] {
+                void* p = nullptr;
+                if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_pf_static_ws)) == hipSuccess)
+                    g_pf_static_base[dev] = static_cast<uint8_t*>(p);
+            });
+            c.ws = g_pf_static_base[dev];
+            c.ws_len = c.ws ? kStaticWsBytes : 0;
+        }
+    }
+    PrefillArgs a = make_args(q, k, v, o, tokens, hq, hkv, pos0);
+    return run(c, a, kv, precision);
 }
 
 }  // namespace brasa

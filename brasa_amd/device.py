@@ -25,6 +25,13 @@ def device_name() -> str:
     return buf.value.decode()
 
 
+def mem_info() -> tuple[int, int]:
+    """(free, total) bytes of the current device."""
+    f, t = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    check(lib().brasa_rt_mem_info(ctypes.byref(f), ctypes.byref(t)))
+    return int(f.value), int(t.value)
+
+
 def synchronize() -> None:
     check(lib().brasa_rt_device_synchronize())
 

@@ -231,3 +231,17 @@ class Kernels:
                              precision: PrefillPrecision, stream=None) -> None:
         check(lib().brasa_flash_attention_with(_ptr(q), _ptr(k), _ptr(v), _ptr(o), shape.c(),
                                                int(precision), _stream(stream or self.stream)))
+
+    @staticmethod
+    def flash_attention_workspace_len(shape: AttnShape, precision: PrefillPrecision) -> int:
+        """Bytes of caller workspace ``flash_attention_ws`` needs (no reference counterpart)."""
+        return int(lib().brasa_flash_attention_workspace_len(shape.c(), int(precision)))
+
+    def flash_attention_ws(self, q, k, v, o, shape: AttnShape, precision: PrefillPrecision,
+                           workspace, workspace_len: int | None = None, stream=None) -> None:
+        """``flash_attention_with`` on a caller-owned workspace (no reference counterpart)."""
+        wlen = (workspace.nbytes if workspace is not None and hasattr(workspace, "nbytes") else 0) \
+            if workspace_len is None else workspace_len
+        check(lib().brasa_flash_attention_ws(_ptr(q), _ptr(k), _ptr(v), _ptr(o), shape.c(),
+                                             int(precision), _ptr(workspace), wlen,
+                                             _stream(stream or self.stream)))

@@ -11,14 +11,16 @@
  *     (crates/metal/src/runtime.rs:255-295), is passed as the already-offset pointer.
  *   - `stream` is a hipStream_t passed as void* (NULL = the default stream). Work is enqueued,
  *     never waited for; ordering is the stream's, as the reference's one in-order command queue.
- *     Calls that share a stream are enqueued from one host thread at a time (the prefill
- *     workspaces of a stream are grown and reused in its order).
- *   - Decode scratch (`partials`) is caller-owned, sized by brasa_decode_partials_len(). The
- *     library's own device state is its arrival counters (the in-kernel split merges of decode
- *     and of prefill's key split; each launch returns the ones it uses to zero) and the
- *     no-allocation entry point's array. Prefill keeps workspaces per (device, stream) for
- *     its key split and for the f16 staging of a q8_0 cache, grown inside the call on its
- *     stream when needed (see brasa_flash_attention_with, brasa_release_workspaces).
+ *   - No call allocates device memory. Decode scratch (`partials`) is caller-owned, sized by
+ *     brasa_decode_partials_len(). The library's own device state is fixed at load: arrival
+ *     counters of the in-kernel split merges (decode, and prefill's key split; each launch
+ *     returns the ones it uses to zero), one slot of them per stream (the first 64 streams used
+ *     on a device each get one, in the order they are first used; a launch on a stream without
+ *     a slot uses a plan that needs no counters: one split per sequence in decode, no key split
+ *     in prefill), the no-allocation decode array and the fixed prefill workspace (see
+ *     brasa_flash_attention_with, brasa_release_workspaces). A graph captured from a stream
+ *     keeps that stream's slot: do not replay it while other work on the same stream, or
+ *     another replay of a graph captured there, is in flight.
  *   - Return value: BRASA_OK (0) or a BRASA_ERR_* code; brasa_last_error() then describes it
  *     (thread-local string, valid until the next call on the same thread).
  *
@@ -129,7 +131,11 @@ int brasa_dequantize_kv_q8(const void* src, float* dst, size_t rows, void* strea
  * hq / hkv in {1, 2, 4, 8} (BRASA_ERR_UNSUPPORTED otherwise, where the reference panics).
  * The result bits depend only on q, the cache rows and lk: the launch layout is a function of
  * lk and the head counts (no tuning knob), and the split merge runs in a fixed order, as the
- * reference requires of every launch width (crates/kernels/tests/launch.rs:119-168).
+ * reference requires of every launch width (crates/kernels/tests/launch.rs:119-168). The
+ * exception is a stream without a counter slot (more than 64 streams in use on the device),
+ * which decodes with one split per sequence: the same result to the decode tolerance, slower.
+ * The split merge counts arrivals in the stream's slot, so launches in flight on different
+ * streams never share counters.
  */
 int brasa_decode_attention_lanes(const float* q, const void* k, const void* v, float* partials,
                                  size_t partials_len, void* o, int o_dtype,
@@ -163,8 +169,8 @@ int brasa_decode_attention(const float* q, const void* k, const void* v, float* 
 /*
  * Ragged batched decode (no counterpart in the reference, which decodes one sequence per call,
  * lib.rs:1110-1164; a caller batching sequences, e.g. a serving scheduler over session.rs:240-245,
- * would otherwise issue one call per sequence). One launch of the split kernel (and one of the
- * merge) covers n sequences: sequence i has one query q[i] (q: [n, hq, 128] f32), its own layer
+ * would otherwise issue one call per sequence). One launch of the split kernel (the split merge
+ * runs inside it) covers up to 64 sequences (more: one launch per 64): sequence i has one query q[i] (q: [n, hq, 128] f32), its own layer
  * caches k[i] / v[i] (HOST arrays of device pointers, same layout as decode_attention_lanes) and
  * lk[i] >= 1 keys (HOST array). o: [n, hq, 128] in o_dtype. Each sequence's result agrees with
  * brasa_decode_attention_lanes on it alone to the decode tolerance, not bit for bit: a launch
@@ -193,10 +199,18 @@ int brasa_decode_attention_batch(const float* q, const void* const* k, const voi
  * after a long cached prefix, e.g. 512 tokens at pos0 16384) splits each tile's keys over up to
  * 8 workgroups; their partials go to a workspace (68 KB per part and query tile). With a q8_0
  * cache and BRASA_PREFILL_F16, the rows read (ceil64(pos0 + tokens) positions) are first
- * dequantised to f16 (each value f16(code * scale)) into a second workspace (512 B per row of K
- * and V), and the f16 kernels run on it. Workspaces are kept per (device, stream), grown with
- * hipMallocAsync / hipFreeAsync on `stream` when a call needs more, and otherwise reused; see
- * brasa_release_workspaces. The result does not depend on the order in which the parts finish.
+ * dequantised to f16 (each value f16(code * scale)) into the workspace (512 B per row of K and
+ * V), and the f16 kernels run on it; small calls convert the same values in registers. When a
+ * group scale lets f16(code * scale) leave the normal f16 range (|scale| >= 516, f16-subnormal,
+ * inf or NaN scales) the call is recomputed by the exact kernel (the reference's F16 numerics:
+ * Q rounded to f16, K / V exact, P f32), which costs one more short launch on every such call.
+ * Like the reference's, this call allocates nothing: its workspace is a fixed 96 MiB device
+ * array of the library, owned by the first stream that needs it (until
+ * brasa_release_workspaces); calls on other streams, or whose plan needs more, run without the
+ * key split or the staging (slower, the same results up to the split's rounding).
+ * brasa_flash_attention_ws takes a caller workspace instead. The key split counts its parts in
+ * the stream's counter slot (see brasa_decode_attention_lanes). The result does not depend on
+ * the order in which the parts finish.
  */
 int brasa_flash_attention_with(const float* q, const void* k, const void* v, void* o,
                                brasa_attn_shape shape, int precision, void* stream);
@@ -204,6 +218,25 @@ int brasa_flash_attention_with(const float* q, const void* k, const void* v, voi
 /* Kernels::flash_attention (lib.rs:1169-1180): brasa_flash_attention_with(.., F16). */
 int brasa_flash_attention(const float* q, const void* k, const void* v, void* o,
                           brasa_attn_shape shape, void* stream);
+
+/*
+ * No counterpart in the reference (its flash_attention encodes onto buffers the caller owns and
+ * needs no scratch; lib.rs:1169-1248). Bytes of workspace brasa_flash_attention_ws needs for
+ * this shape and precision: the key split's partials and the q8_0 staging the call's plan uses
+ * (0 when it uses neither, or for an invalid shape).
+ */
+size_t brasa_flash_attention_workspace_len(brasa_attn_shape shape, int precision);
+
+/*
+ * brasa_flash_attention_with on a caller-owned device workspace of workspace_len bytes (at least
+ * brasa_flash_attention_workspace_len; BRASA_ERR_SCRATCH otherwise), for callers on any stream
+ * that want the full plan. Allocates nothing. The same kernels and plan as the fixed-workspace
+ * call, so the results are bit-identical to it. Calls in flight at the same time need distinct
+ * workspaces.
+ */
+int brasa_flash_attention_ws(const float* q, const void* k, const void* v, void* o,
+                             brasa_attn_shape shape, int precision, void* workspace,
+                             size_t workspace_len, void* stream);
 
 /*
  * RopeTable (lib.rs:1365-1386): device arrays cos/sin [max_pos, dim / 2] (f32) built from
@@ -253,12 +286,12 @@ int brasa_qk_norm_rope_store(int kv, float* q, float* k, const float* v, const f
                              void* k_dst, void* v_dst, brasa_attn_shape shape, void* stream);
 
 /*
- * No counterpart in the reference. Frees the prefill workspaces the library keeps, one per
- * (device, stream) and kind: the key-split partials and the f16 staging of a q8_0 cache (see
- * brasa_flash_attention_with). They are grown on demand and otherwise kept from call to call;
- * this call waits for the devices' work and releases them (a later prefill call allocates
- * again). Call it only while no prefill call is being enqueued, e.g. before destroying the
- * streams they were used on, or at shutdown.
+ * No counterpart in the reference. Returns the library's per-stream state to its initial
+ * condition: the stream -> counter slot assignments (decode and prefill split merges) and the
+ * ownership of the fixed prefill workspace. Call it only while no call of this library is in
+ * flight or being enqueued (e.g. before destroying streams whose handles may be reused), so that
+ * a new stream never inherits a slot whose counters a running launch still uses. Frees nothing:
+ * the library holds no allocations.
  */
 int brasa_release_workspaces(void);
 
@@ -273,6 +306,13 @@ int brasa_release_workspaces(void);
  * set it only while no prefill call is being enqueued on another thread.
  */
 int brasa_test_set_prefill_layout(int variant, int pair, int parts);
+
+/*
+ * Test hook (no counterpart in the reference). The counter slot of `stream` on `device` that the
+ * split merges use (assigning one on first use, as a launch would), or -1 when the device's 64
+ * slots are taken. Needs no GPU.
+ */
+int brasa_test_stream_slot(int device, void* stream, int* slot);
 
 #ifdef BRASA_TIMELINE_BUILD
 /*

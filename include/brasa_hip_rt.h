@@ -36,6 +36,8 @@ int brasa_rt_event_destroy(void* event);
 int brasa_rt_event_record(void* event, void* stream);
 int brasa_rt_event_elapsed_ms(float* ms, void* start, void* stop);
 int brasa_rt_event_synchronize(void* event);
+/* Free and total device memory of the current device (hipMemGetInfo). */
+int brasa_rt_mem_info(size_t* free_bytes, size_t* total_bytes);
 
 /*
  * Synthetic N(0, 1) f32 values for benchmarks: out[i] for i < n is a Box-Muller transform of a

@@ -226,3 +226,64 @@ def test_prefill_layout_hook_validates():
         with pytest.raises(BrasaError):
             check(lib().brasa_test_set_prefill_layout(*bad))
     check(lib().brasa_test_set_prefill_layout(0, 1, 1))
+
+
+def test_stream_slots():
+    """Counter slots are per stream: a stream keeps its slot, distinct streams get distinct
+    slots, the 65th stream on a device gets none (-1), hipStreamPerThread gets one per host
+    thread, and brasa_release_workspaces() starts the assignment over. (Stream handles are
+    only keys here; no GPU is touched.)"""
+    import threading
+    from brasa_amd._lib import check
+
+    def slot(dev, handle):
+        s = ctypes.c_int(-2)
+        check(lib().brasa_test_stream_slot(dev, handle, ctypes.byref(s)))
+        return s.value
+
+    dev = 63  # a device index no other test uses
+    check(lib().brasa_release_workspaces())
+    first = [slot(dev, 0x5000 + 16 * i) for i in range(64)]
+    assert sorted(first) == list(range(64))
+    assert [slot(dev, 0x5000 + 16 * i) for i in range(64)] == first  # stable
+    assert slot(dev, 0x9000) == -1                                   # all 64 taken
+    assert slot(dev - 1, 0x9000) == 0                                # per device
+    check(lib().brasa_release_workspaces())
+    assert slot(dev, 0x9000) == 0
+    per_thread = 2  # hipStreamPerThread: one stream per live host thread
+    got = []
+    bar = threading.Barrier(3)
+
+    def look():
+        got.append(slot(dev, per_thread))
+        bar.wait()  # every thread alive until all have looked up (thread ids can be reused)
+
+    ts = [threading.Thread(target=look) for _ in range(3)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert sorted(got) == [1, 2, 3]
+    check(lib().brasa_release_workspaces())
+    with pytest.raises(Exception):
+        check(lib().brasa_test_stream_slot(64, None, ctypes.byref(ctypes.c_int())))
+
+
+def test_prefill_workspace_len():
+    """Workspace sizes of brasa_flash_attention_ws: none for a full launch, the key split's
+    partials for a short chunk after a long prefix, the f16 staging (512 B per row of K and V
+    read) plus its key split for q8_0."""
+    from brasa_amd import AttnShape, Kernels, PrefillPrecision
+    wl = Kernels.flash_attention_workspace_len
+    F16 = PrefillPrecision.F16
+    assert wl(AttnShape(2048, 32, 8, 128, 0, KvType.F16), F16) == 0
+    assert wl(AttnShape(2048, 32, 8, 128, 0, KvType.F16), PrefillPrecision.F32) == 0
+    # 512 tokens after 16384: 128 workgroups, two key parts of 68 KB per query tile
+    assert wl(AttnShape(512, 32, 8, 128, 16384, KvType.F16), F16) == 128 * 2 * 4 * 17 * 64 * 16
+    staging = 2048 * 8 * 128 * 2 * 2
+    assert wl(AttnShape(2048, 32, 8, 128, 0, KvType.Q8_0), F16) == staging
+    assert wl(AttnShape(2048, 32, 8, 128, 0, KvType.Q8_0), PrefillPrecision.F16_PF32) == 0
+    assert wl(AttnShape(512, 32, 8, 128, 16384, KvType.Q8_0), F16) == \
+        16896 * 8 * 128 * 2 * 2 + 128 * 2 * 4 * 17 * 64 * 16
+    assert wl(AttnShape(0, 32, 8, 128, 0, KvType.F16), F16) == 0
+    assert wl(AttnShape(16, 32, 8, 64, 0, KvType.F16), F16) == 0  # invalid shape

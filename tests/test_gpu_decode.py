@@ -10,6 +10,7 @@ import pytest
 
 import oracle
 from brasa_amd import AttnShape, BrasaError, Kernels, KvType, OutDType, decode_partials_len
+from brasa_amd._lib import lib
 from brasa_amd.device import DeviceBuffer, synchronize
 from gpu_util import DIM, HKV, HQ, KvPair
 
@@ -183,3 +184,40 @@ def test_decode_q8_small_scales(vscale):
         w = oracle.worst(got, want, vmax)
         print(f"q8 scale {vscale} pos0 {pos0}: worst {w:.2e}")
         assert w <= 1e-5, w
+
+
+def test_decode_stream_without_counter_slot():
+    """With all 64 counter slots of the device taken, a launch on another stream decodes with one
+    split per head group (no merge, no counters): still at the reference's bar, and its result
+    matches the split launch's to the decode tolerance. brasa_release_workspaces() frees the
+    slots again."""
+    import ctypes
+    from brasa_amd.device import Stream
+    k = Kernels()
+    rng = oracle.Rng(64)
+    pos0 = 4095
+    q = rng.vec(HQ * DIM, 2.0)
+    cache = KvPair(KvType.F16, rng.vec((pos0 + 1) * HKV * DIM, 2.0),
+                   rng.vec((pos0 + 1) * HKV * DIM, 3.0))
+    _say("decode on a stream without a counter slot")
+    split = run_decode(k, "lanes", q, cache, HQ, HKV, pos0)
+    s = ctypes.c_int()
+    for i in range(64):  # fill every free slot of device 0 with stand-in stream keys
+        assert lib().brasa_test_stream_slot(0, 0x7000 + 16 * i, ctypes.byref(s)) == 0
+    try:
+        st = Stream()
+        assert lib().brasa_test_stream_slot(0, st.handle, ctypes.byref(s)) == 0
+        assert s.value == -1
+        gq = DeviceBuffer.from_array(q)
+        part = DeviceBuffer(4 * decode_partials_len(HQ, pos0 + 1))
+        o = DeviceBuffer(HQ * DIM * 4)
+        k.decode_attention_lanes(gq, cache.kbuf, cache.vbuf, part, o,
+                                 AttnShape(1, HQ, HKV, DIM, pos0, KvType.F16), stream=st)
+        st.synchronize()
+        got = o.download(np.float32).reshape(HQ, DIM)
+    finally:
+        synchronize()
+        assert lib().brasa_release_workspaces() == 0
+    want, vmax = oracle.attention(q, cache.k, cache.v, 1, HQ, HKV, DIM, pos0)
+    assert oracle.worst(got, want, vmax) <= 1e-5
+    assert np.max(np.abs(got - split)) <= 1e-5 * float(vmax.max())

@@ -299,20 +299,135 @@ def test_flash_q8_equals_f16_on_dequantised_rows(tokens, pos0):
 
 
 def test_release_workspaces():
-    """The kept workspaces (q8_0 staging, key-split partials) can be released between calls:
-    the next calls allocate again and give the same bits."""
+    """brasa_release_workspaces() between calls (the fixed workspace changes owner, the stream's
+    counter slot is assigned again): the next calls give the same bits."""
     k = Kernels()
     rng = oracle.Rng(98)
     tokens, pos0 = 64, 8192
     cap = (pos0 + tokens + 63) // 64 * 64
     q = rng.vec(tokens * HQ * DIM, 2.0)
     q8 = KvPair(KvType.Q8_0, rng.vec(cap * HKV * DIM, 2.0), rng.vec(cap * HKV * DIM, 3.0))
-    _say("prefill workspaces released between calls")
+    _say("prefill after brasa_release_workspaces")
     a = run_prefill(k, q, q8, tokens, HQ, HKV, pos0, PrefillPrecision.F16)
     assert lib().brasa_release_workspaces() == 0
     b = run_prefill(k, q, q8, tokens, HQ, HKV, pos0, PrefillPrecision.F16)
     assert lib().brasa_release_workspaces() == 0
     assert np.array_equal(a, b)
+
+
+WS_CASES = [(512, 16384, KvType.F16), (512, 16384, KvType.Q8_0), (2048, 0, KvType.Q8_0),
+            (64, 8192, KvType.Q8_0), (100, 7, KvType.F16)]
+
+
+@pytest.mark.parametrize("tokens,pos0,kv", WS_CASES)
+def test_flash_workspace_entry_point(tokens, pos0, kv):
+    """brasa_flash_attention_ws on a caller workspace of brasa_flash_attention_workspace_len
+    bytes gives the bits of the reference-signature call (the same plan on the library's fixed
+    workspace): a key-split chunk (f16 and q8_0), q8_0 staging, a q8_0-kernel split and a call
+    that needs no workspace; one byte less is BRASA_ERR_SCRATCH."""
+    from brasa_amd import BrasaError
+    k = Kernels()
+    rng = oracle.Rng(61)
+    cap = (pos0 + tokens + 63) // 64 * 64
+    q = rng.vec(tokens * HQ * DIM, 2.0)
+    cache = KvPair(kv, rng.vec(cap * HKV * DIM, 2.0), rng.vec(cap * HKV * DIM, 3.0))
+    shape = AttnShape(tokens, HQ, HKV, DIM, pos0, kv)
+    need = Kernels.flash_attention_workspace_len(shape, PrefillPrecision.F16)
+    _say(f"prefill workspace entry T={tokens} pos0={pos0} kv={kv.name_str}: {need} bytes")
+    want = run_prefill(k, q, cache, tokens, HQ, HKV, pos0, PrefillPrecision.F16)
+    gq = DeviceBuffer.from_array(q)
+    ws = DeviceBuffer(max(need, 256))
+    ws.fill(0xFF)
+    o = DeviceBuffer(tokens * HQ * DIM * 2)
+    k.flash_attention_ws(gq, cache.kbuf, cache.vbuf, o, shape, PrefillPrecision.F16, ws, need)
+    synchronize()
+    assert np.array_equal(o.download(np.uint16).reshape(tokens, HQ, DIM), want)
+    if need > 0:
+        with pytest.raises(BrasaError) as e:
+            k.flash_attention_ws(gq, cache.kbuf, cache.vbuf, o, shape, PrefillPrecision.F16, ws,
+                                 need - 1)
+        assert e.value.code == 2
+
+
+def test_flash_calls_allocate_nothing():
+    """After one warm-up of each plan, further prefill calls -- the reference-signature ones
+    (fixed workspace: key split, q8_0 staging) and the caller-workspace one -- leave the
+    device's free memory unchanged: nothing is allocated inside a call."""
+    from brasa_amd.device import mem_info
+    k = Kernels()
+    rng = oracle.Rng(62)
+    runs = []
+    for tokens, pos0, kv in [(512, 16384, KvType.F16), (384, 0, KvType.Q8_0), (64, 8192, KvType.Q8_0)]:
+        cap = (pos0 + tokens + 63) // 64 * 64
+        q = DeviceBuffer.from_array(rng.vec(tokens * HQ * DIM, 2.0))
+        cache = KvPair(kv, rng.vec(cap * HKV * DIM, 2.0), rng.vec(cap * HKV * DIM, 3.0))
+        o = DeviceBuffer(tokens * HQ * DIM * 2)
+        runs.append((q, cache, o, AttnShape(tokens, HQ, HKV, DIM, pos0, kv)))
+    need = max(Kernels.flash_attention_workspace_len(sh, PrefillPrecision.F16) for *_, sh in runs)
+    ws = DeviceBuffer(need)
+
+    def all_calls():
+        for q, cache, o, sh in runs:
+            k.flash_attention(q, cache.kbuf, cache.vbuf, o, sh)
+            k.flash_attention_ws(q, cache.kbuf, cache.vbuf, o, sh, PrefillPrecision.F16, ws, need)
+        synchronize()
+
+    _say("prefill: free device memory across calls")
+    all_calls()
+    free0, _ = mem_info()
+    for _ in range(3):
+        all_calls()
+    free1, _ = mem_info()
+    assert free1 == free0, (free0, free1)
+
+
+Q8_RANGE_CASES = [(64, 500, "k_large"), (64, 500, "v_large"), (64, 500, "tiny"),
+                  (384, 0, "k_large"), (384, 0, "v_large"), (384, 0, "tiny")]
+
+
+@pytest.mark.parametrize("tokens,pos0,kind", Q8_RANGE_CASES)
+def test_flash_q8_scales_outside_f16(tokens, pos0, kind):
+    """q8_0 F16 prefill with group scales for which f16(code * scale) leaves the normal f16
+    range: K scales above 516 (products past 65504), one V group scaled past 516 (its row keeps
+    a small weight, so the output stays in f16 range), and every scale f16-subnormal. Both the
+    in-register kernel (64 tokens) and the dequantised-rows path (384 tokens) flag them and the
+    exact kernel recomputes the call: the reference's F16 numerics (K / V exact, Q rounded to
+    f16, P f32), so its own bar worst_f16 <= 1e-5 (attention.rs:105) against attention_q16 over
+    the exact dequantised cache, and the BASELINE.json bar."""
+    k = Kernels()
+    rng = oracle.Rng(63)
+    cap = (pos0 + tokens + 63) // 64 * 64
+    q = rng.vec(tokens * HQ * DIM, 2.0)
+    kk = rng.vec(cap * HKV * DIM, 2.0)
+    vv = rng.vec(cap * HKV * DIM, 3.0)
+    if kind == "k_large":
+        kk = kk * np.float32(4e4)          # |k| up to 8e4: scales ~630
+        q = q * np.float32(1e-4)           # scores stay moderate
+    elif kind == "v_large":
+        vv[(10 * HKV + 3) * DIM + 5] = 66000.0  # one group scale f16(66000 / 127) = 519.5
+    else:
+        # |x| < 7.7e-3: every scale below 2^-14, f16-subnormal (outputs stay normal f16 numbers,
+        # whose rounding worst_f16 discounts)
+        kk = kk * np.float32(2e-3)
+        vv = vv * np.float32(2e-3)
+    cache = KvPair(KvType.Q8_0, kk, vv)
+    _say(f"prefill q8_0 scales outside f16 ({kind}) T={tokens} pos0={pos0}")
+    oh = run_prefill(k, q, cache, tokens, HQ, HKV, pos0, PrefillPrecision.F16)
+    ref16, vmax = oracle.attention(q, cache.k, cache.v, tokens, HQ, HKV, DIM, pos0, q16=True)
+    got = oracle.f16_to_f32(oh)
+    assert np.all(np.isfinite(got))
+    w = oracle.worst_f16(oh, ref16, vmax)
+    if kind == "tiny":
+        # outputs of rows with few keys can be f16-subnormal (v itself is ~1e-5 there), where
+        # the f16 output rounding is up to 2^-25 absolute rather than the 2^-11 relative that
+        # worst_f16 discounts: discount both
+        d = np.abs(got.astype(np.float64) - ref16) - np.abs(ref16) * 2.0**-11 - 2.0**-25
+        w = float((np.maximum(d, 0.0) / np.maximum(vmax.reshape(d.shape), 1e-30)).max())
+    a, r = bars(got, ref16)
+    print(f"q8 {kind}: worst_f16 {w:.2e} max-abs {a:.2e} max-rel {r:.2e}")
+    assert w <= 1e-5, w
+    if kind != "v_large":  # (outputs near the large V value are far above the f16 bar's scale)
+        assert a <= 2e-3 and r <= 1e-2, (a, r)
 
 
 def test_flash_key_split_chosen_by_size():
