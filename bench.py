@@ -166,8 +166,25 @@ def bench_ragged(k, stream, steps, warmup, seed=12345):
             "GBps_batched": total / tb / 1e9}
 
 
+def sustained_calls(fn, stream: Stream, blocks: int = 15, per_block: int = 10) -> dict:
+    """blocks x per_block back-to-back calls, one event pair per block (nothing waits between
+    blocks): per-call µs of every block, their median and the last block's. Shows the rate once
+    the clock has settled under continuous load."""
+    stream.synchronize()
+    evs = [Event() for _ in range(blocks + 1)]
+    evs[0].record(stream)
+    for b in range(blocks):
+        for _ in range(per_block):
+            fn(stream)
+        evs[b + 1].record(stream)
+    evs[-1].synchronize()
+    per = [evs[b].elapsed_ms(evs[b + 1]) * 1e3 / per_block for b in range(blocks)]
+    return {"calls": blocks * per_block, "us_median": float(np.median(per)),
+            "us_last_block": per[-1], "us_blocks": [round(x, 2) for x in per]}
+
+
 def bench_prefill(k, stream, tokens, pos0, kv, steps, warmup, seed=3,
-                  precision=PrefillPrecision.F16):
+                  precision=PrefillPrecision.F16, sustained=False):
     """Causal prefill of `tokens` queries at positions pos0.. over a cache of ceil64(pos0 +
     tokens) positions. As BASELINE.json config 4 describes the inputs: Q and K are N(0, 1) put
     through per-head RMSNorm (weight 1, eps 1e-6) and RoPE-NeoX (theta 1e6) at their positions
@@ -199,11 +216,20 @@ def bench_prefill(k, stream, tokens, pos0, kv, steps, warmup, seed=3,
     tf = prefill_flops(tokens, pos0) / t / 1e12
     log(f"prefill kv={kv.name_str} {precision.name} T={tokens} pos0={pos0}: {t * 1e6:.1f} µs, "
         f"{tf:.1f} TFLOP/s")
+    out = {"us": t * 1e6, "TFLOPs": tf, "flop": prefill_flops(tokens, pos0),
+           "frac_mfma_f16_peak": tf / MFMA_F16_PEAK_TFLOPS}
+    if sustained:
+        sus = sustained_calls(lambda s: k.flash_attention_with(q, kb, vb, o, shape, precision, s),
+                              stream)
+        sus["TFLOPs_median"] = prefill_flops(tokens, pos0) / (sus["us_median"] * 1e-6) / 1e12
+        sus["frac_mfma_f16_peak_median"] = sus["TFLOPs_median"] / MFMA_F16_PEAK_TFLOPS
+        log(f"prefill sustained ({sus['calls']} calls): median {sus['us_median']:.1f} µs, "
+            f"last block {sus['us_last_block']:.1f} µs")
+        out["sustained"] = sus
     for b in (kb, vb, q, o, ones):
         b.free()
     table.free()
-    return {"us": t * 1e6, "TFLOPs": tf, "flop": prefill_flops(tokens, pos0),
-            "frac_mfma_f16_peak": tf / MFMA_F16_PEAK_TFLOPS}, t
+    return out, t
 
 
 def bench_qkv(k, stream, tokens, kv, steps, warmup, seed=21):
@@ -321,7 +347,7 @@ def profile_run(k: Kernels, stream: Stream, what: str) -> int:
     if what in decode_cases:
         lk, kv = decode_cases[what]
         layers = DecodeLayers(k, lk, kv, stream)
-        for _ in range(3):
+        for _ in range(6):  # the first step is the cold one (brasa_amd.trace_summary drops it)
             layers.step(stream)
         stream.synchronize()
         layers.free()
@@ -358,7 +384,8 @@ def main() -> int:
         return profile_run(k, stream, args.profile)
 
     head, t_step = bench_decode(k, stream, 16384, KvType.F16, args.steps, args.warmup)
-    pre2k, _ = bench_prefill(k, stream, 2048, 0, KvType.F16, max(args.steps, 20), args.warmup)
+    pre2k, _ = bench_prefill(k, stream, 2048, 0, KvType.F16, max(args.steps, 20), args.warmup,
+                             sustained=True)
     extra_decode, extra_prefill = {}, {}
     if not args.quick:
         for lk in (4096, 32768):

@@ -1680,40 +1680,42 @@ __global__ void __launch_bounds__(256)
 prefill_exact_kernel(PrefillArgs a) {
     if (a.gate && *a.gate != a.tag) return;
     const int lane = threadIdx.x & 63;
-    const int rw = blockIdx.x * 4 + (threadIdx.x >> 6);  // query token * hq + query head
-    if (rw >= a.tokens * a.hq) return;
-    const int t = rw / a.hq, h = rw - t * a.hq, kh = h / a.group, d = 2 * lane;
-    const f32x2 qv = *reinterpret_cast<const f32x2*>(a.q + (size_t)rw * kDim + d);
-    const float q0 = h2f(f2h(as_f32(qv.x * a.scale))), q1 = h2f(f2h(as_f32(qv.y * a.scale)));
-    float m = -INFINITY, l = 0.0f, o0 = 0.0f, o1 = 0.0f;
-    const int kend = a.pos0 + t + 1;
-    for (int j = 0; j < kend; ++j) {
-        const size_t row = (size_t)j * a.hkv + kh;
-        const f32x2 kk = row_pair<KV>(a.k, row, d);
-        const f32x2 vv = row_pair<KV>(a.v, row, d);
-        float sc = row16_sum(fmaf(q0, kk.x, q1 * kk.y));
-        sc += __shfl_xor(sc, 16, 64);
-        sc += __shfl_xor(sc, 32, 64);
-        const float x = sc * kLog2e;
-        const float mn = fmaxf(m, x);
-        const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
-        const float p = __builtin_amdgcn_exp2f(x - mn);
-        l = fmaf(l, alpha, p);
-        o0 = fmaf(o0, alpha, p * vv.x);
-        o1 = fmaf(o1, alpha, p * vv.y);
-        m = mn;
+    // query token * hq + query head, grid-stride (a small grid: the common launch only reads
+    // the gate)
+    for (int rw = blockIdx.x * 4 + (threadIdx.x >> 6); rw < a.tokens * a.hq; rw += gridDim.x * 4) {
+        const int t = rw / a.hq, h = rw - t * a.hq, kh = h / a.group, d = 2 * lane;
+        const f32x2 qv = *reinterpret_cast<const f32x2*>(a.q + (size_t)rw * kDim + d);
+        const float q0 = h2f(f2h(as_f32(qv.x * a.scale))), q1 = h2f(f2h(as_f32(qv.y * a.scale)));
+        float m = -INFINITY, l = 0.0f, o0 = 0.0f, o1 = 0.0f;
+        const int kend = a.pos0 + t + 1;
+        for (int j = 0; j < kend; ++j) {
+            const size_t row = (size_t)j * a.hkv + kh;
+            const f32x2 kk = row_pair<KV>(a.k, row, d);
+            const f32x2 vv = row_pair<KV>(a.v, row, d);
+            float sc = row16_sum(fmaf(q0, kk.x, q1 * kk.y));
+            sc += __shfl_xor(sc, 16, 64);
+            sc += __shfl_xor(sc, 32, 64);
+            const float x = sc * kLog2e;
+            const float mn = fmaxf(m, x);
+            const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+            const float p = __builtin_amdgcn_exp2f(x - mn);
+            l = fmaf(l, alpha, p);
+            o0 = fmaf(o0, alpha, p * vv.x);
+            o1 = fmaf(o1, alpha, p * vv.y);
+            m = mn;
+        }
+        const float inv = 1.0f / l;
+        *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.o) + (size_t)rw * kDim + d) =
+            (uint32_t)f2h(o0 * inv) | ((uint32_t)f2h(o1 * inv) << 16);
     }
-    const float inv = 1.0f / l;
-    *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.o) + (size_t)rw * kDim + d) =
-        (uint32_t)f2h(o0 * inv) | ((uint32_t)f2h(o1 * inv) << 16);
 }
 
 template <int KV>
 int launch_exact(PfCtx& c, const PrefillArgs& a) {
     if (c.measure) return BRASA_OK;
     const long long rows = (long long)a.tokens * a.hq;
-    hipLaunchKernelGGL(prefill_exact_kernel<KV>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
-                       c.stream, a);
+    hipLaunchKernelGGL(prefill_exact_kernel<KV>, dim3((unsigned)std::min<long long>((rows + 3) / 4, 256)),
+                       dim3(256), 0, c.stream, a);
     return check_launch("prefill_exact_kernel");
 }
 

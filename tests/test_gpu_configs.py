@@ -18,6 +18,15 @@ from brasa_amd import AttnShape, Kernels, KvType, PrefillPrecision, decode_parti
 from brasa_amd.device import DeviceBuffer, synchronize
 from gpu_util import DIM, HKV, HQ, KvPair, bars, f16_normal, post_norm_rope
 
+# worst_f16 (attention.rs:12-23: error over max|v|, the f16 output rounding discounted) that the
+# F16 hot path (P rounded to f16 for the matrix cores; q8_0 values as f16(code * scale)) holds at
+# the BASELINE.json prefill configurations, measured 7.1e-5 / 8.0e-5 / 2.7e-6 (f16: T 2048,
+# 8192, 512 at 16384) and 4.0e-4 / 5.0e-6 (q8_0: T 2048, 512 at 16384), held with ~1.3-1.5x
+# margin (deterministic results). The reference's F16 kernel keeps P in f32 and reads q8_0 values
+# exactly and is held to 1e-5 (attention.rs:99-104); F16_PF32 is held to that here.
+F16_WORST_BOUND = 1.2e-4
+Q8_F16_WORST_BOUND = 6e-4
+
 pytestmark = pytest.mark.gpu
 
 
@@ -104,11 +113,13 @@ def test_prefill_config(tokens, pos0):
     assert np.all(np.isfinite(got))
     rows = _tile_rows(tokens, tokens + pos0)
     _say(f"prefill config T={tokens} pos0={pos0}: oracle on {len(rows)} rows (one per tile)")
-    want, _ = _oracle_rows(q, cache, tokens, pos0, rows)
+    want, vmax = _oracle_rows(q, cache, tokens, pos0, rows)
     a, r = bars(got[rows], want)
+    w = oracle.worst_f16(o.download(np.uint16).reshape(tokens, HQ, DIM)[rows], want, vmax)
     print(f"prefill T={tokens} pos0={pos0}, {len(rows)} rows x {HQ} heads: max-abs {a:.2e} "
-          f"max-rel {r:.2e}")
+          f"max-rel {r:.2e} worst_f16 {w:.2e}")
     assert a <= 2e-3 and r <= 1e-2
+    assert w <= F16_WORST_BOUND, w
 
 
 def test_prefill_config_f16_pf32_2048():
@@ -164,8 +175,11 @@ def test_prefill_config_q8_every_tile(tokens, pos0):
     synchronize()
     got = oracle.f16_to_f32(o.download(np.uint16)).reshape(tokens, HQ, DIM)
     rows = _tile_rows(tokens, 5 + tokens)
-    want, _ = _oracle_rows(q, cache, tokens, pos0, rows)
+    want, vmax = _oracle_rows(q, cache, tokens, pos0, rows)
     a, r = bars(got[rows], want)
-    print(f"prefill q8 T={tokens} pos0={pos0}, {len(rows)} rows: max-abs {a:.2e} max-rel {r:.2e}")
+    w = oracle.worst_f16(o.download(np.uint16).reshape(tokens, HQ, DIM)[rows], want, vmax)
+    print(f"prefill q8 T={tokens} pos0={pos0}, {len(rows)} rows: max-abs {a:.2e} max-rel {r:.2e} "
+          f"worst_f16 {w:.2e}")
     assert a <= 2e-3 and r <= 1e-2
+    assert w <= Q8_F16_WORST_BOUND, w
 

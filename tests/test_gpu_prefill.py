@@ -23,6 +23,13 @@ from gpu_util import DIM, HKV, HQ, KvPair, bars
 pytestmark = pytest.mark.gpu
 
 KVS = [KvType.F32, KvType.F16, KvType.Q8_0]
+# worst_f16 of the F16 hot path (P rounded to f16; q8_0 values as f16(code * scale)) against the
+# reference's attention_q16 over the exact cache values, on the reference's own case matrix:
+# measured 1.68e-4 (f32 cache), 1.87e-4 (f16), 5.34e-4 (q8_0), held with ~1.3x margin (the
+# results are deterministic). The reference's F16 kernel (P f32, exact q8_0 values) is held to
+# 1e-5 (attention.rs:99-104); F16_PF32 below meets that bar. A wrong scale, group or key index
+# costs errors of the order of the values themselves.
+F16_WORST_BOUND = {KvType.F32: 2.5e-4, KvType.F16: 2.5e-4, KvType.Q8_0: 7e-4}
 CASES = [(9, 0), (5, 11), (1, 0), (1, 1500), (33, 40), (64, 448), (32, 0), (100, 7)]
 
 
@@ -68,6 +75,7 @@ def test_flash_attention_gqa_causal(kv):
     print(f"flash KV {kv.name_str}: F16 max-abs {mabs:.2e} max-rel {mrel:.2e} "
           f"worst_f16 {w16:.2e} vs-unrounded {w_raw:.2e}; F16_PF32 {w_pf32:.2e}; F32 {w32:.2e}")
     assert mabs <= 2e-3 and mrel <= 1e-2, (mabs, mrel)
+    assert w16 <= F16_WORST_BOUND[kv], w16
     assert w_raw <= 2e-3, w_raw
     assert w_pf32 <= 1e-5, w_pf32
     assert w32 <= 1e-5, w32
