@@ -1714,7 +1714,7 @@ template <int KV>
 int launch_exact(PfCtx& c, const PrefillArgs& a) {
     if (c.measure) return BRASA_OK;
     const long long rows = (long long)a.tokens * a.hq;
-    hipLaunchKernelGGL(prefill_exact_kernel<KV>, dim3((unsigned)std::min<long long>((rows + 3) / 4, 256)),
+    hipLaunchKernelGGL(prefill_exact_kernel<KV>, dim3((unsigned)std::min<long long>((rows + 3) / 4, 64)),
                        dim3(256), 0, c.stream, a);
     return check_launch("prefill_exact_kernel");
 }

@@ -146,12 +146,16 @@ int brasa_decode_attention_lanes(const float* q, const void* k, const void* v, f
  * for callers that cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc): the split partials live in a fixed array inside the
  * library, BRASA_DECODE_NOALLOC_FLOATS floats (4 MiB) per device, held until the process ends.
- * A call needs hq * splits * 130 floats, where the launch plan keeps splits <= 256 / hkv (with
- * 8 KV heads: 32 splits, 133,120 floats for hq 32, at any length); a call needing more fails
- * with BRASA_ERR_SCRATCH. The call allocates nothing.
+ * A call needs hq * splits * 130 floats, where the launch plan keeps splits <= 256 * h / hkv
+ * for h head groups per workgroup (h <= 4, h * hq / hkv <= 16; with 8 KV heads: 32 splits,
+ * 133,120 floats for hq 32, at any length), so no valid shape needs more than 16 * 256 * 130
+ * floats; a call needing more would fail with BRASA_ERR_SCRATCH. The call allocates nothing.
  * Every call on one device shares the array: calls that overlap on one GPU (different streams
- * without ordering) race and give wrong results. Same results, bit for bit, as
- * brasa_decode_attention_lanes on the same arguments.
+ * without ordering, or graph replays concurrent with other decode calls) race and give wrong
+ * results. Its split merge counts arrivals in the calling stream's counter slot, like
+ * brasa_decode_attention_lanes; a graph captured from a stream keeps that slot (see the
+ * conventions above). Same results, bit for bit, as brasa_decode_attention_lanes on the same
+ * arguments.
  */
 #define BRASA_DECODE_NOALLOC_FLOATS (1 << 20)
 int brasa_decode_attention_lanes_noalloc(const float* q, const void* k, const void* v, void* o,

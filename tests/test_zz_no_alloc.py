@@ -41,3 +41,27 @@ def test_noalloc_matches_scratch_entry_point(kv):
         if out == OutDType.F32:
             want, vmax = oracle.attention(q, cache.k, cache.v, 1, HQ, HKV, DIM, pos0)
             assert oracle.worst(got.reshape(HQ, DIM), want, vmax) <= 1e-5
+
+
+@pytest.mark.parametrize("hq,hkv", [(32, 32), (32, 4), (16, 8)])
+def test_noalloc_other_groups(hq, hkv):
+    """Other GQA groups (1, 8, 2): the no-allocation call gives the scratch call's bits, twice
+    in a row with the second call smaller, and holds the reference's bar."""
+    k = Kernels()
+    rng = oracle.Rng(92)
+    for pos0 in [9000, 300]:
+        lk = pos0 + 1
+        print(f"noalloc hq={hq} hkv={hkv} pos0={pos0}", flush=True)
+        q = rng.vec(hq * DIM, 2.0)
+        cache = KvPair(KvType.F16, rng.vec(lk * hkv * DIM, 2.0), rng.vec(lk * hkv * DIM, 3.0))
+        shape = AttnShape(1, hq, hkv, DIM, pos0, KvType.F16)
+        gq = DeviceBuffer.from_array(q)
+        o_ref, o_na = DeviceBuffer(hq * DIM * 4), DeviceBuffer(hq * DIM * 4)
+        part = DeviceBuffer(4 * decode_partials_len(hq, lk))
+        k.decode_attention_lanes(gq, cache.kbuf, cache.vbuf, part, o_ref, shape)
+        k.decode_attention_lanes_noalloc(gq, cache.kbuf, cache.vbuf, o_na, shape)
+        synchronize()
+        ref, got = o_ref.download(np.float32), o_na.download(np.float32)
+        assert np.array_equal(ref.view(np.uint32), got.view(np.uint32))
+        want, vmax = oracle.attention(q, cache.k, cache.v, 1, hq, hkv, DIM, pos0)
+        assert oracle.worst(got.reshape(hq, DIM), want, vmax) <= 1e-5
