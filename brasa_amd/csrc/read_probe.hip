@@ -1,0 +1,149 @@
+// Read-only probes of the decode access pattern (measurement tool, not part of the library).
+//
+// The fp16 decode at 16384 keys reads 2 x 16384 x 8 x 256 bytes (67.1 MB) per layer. These
+// kernels read exactly those bytes and do no math, so their time is what the memory system
+// gives each access pattern; 36 layer caches are rotated (2.4 GB, past the 256 MB MALL), 36
+// back-to-back launches are timed with HIP events, the median of 7 runs is printed per layer.
+//   * one / two / four KV heads per workgroup: 256 workgroups of 8 wave64, every wave reads two
+//     32-key blocks of K (16-byte loads into registers) and V (16-byte copies into LDS), the
+//     decode kernel's instructions, for 1, 2 or 4 adjacent KV heads per workgroup;
+//   * contiguous: the same instructions over whole 2 KB key rows (64 keys x 8 heads per workgroup);
+//   * stream: a grid-stride read of both caches, 16 bytes per lane, the plain streaming ceiling.
+// Build: make -C brasa_amd/csrc read_probe; run: _build/read_probe (one GPU).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <vector>
+
+#include "common.hpp"
+
+using namespace brasa;
+
+namespace {
+
+constexpr int kKeys = 16384, kHeads = 8, kRow = 256, kLayers = 36;
+constexpr size_t kCache = (size_t)kKeys * kHeads * kRow;
+
+__device__ __forceinline__ u32x4 load16(const uint8_t* p) {
+    u32x4 r;
+    asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(r) : "v"(p) : "memory");
+    return r;
+}
+
+// HPW heads per workgroup (1, 2, 4), or 8 for whole contiguous key rows.
+template <int HPW>
+__global__ void __launch_bounds__(512) pattern_kernel(const uint8_t* K, const uint8_t* V, unsigned* out) {
+    __shared__ __attribute__((aligned(16))) uint16_t s_v[8][2][4096];
+    const int b = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int c16 = lane & 15, u = lane >> 4;
+    u32x4 kx[2][8];
+    for (int blk = 0; blk < 2; ++blk) {
+        const uint8_t *kr[2], *vr[8];
+        if constexpr (HPW == 8) {
+            // 4 whole key rows (8 KB) per wave and block: keys 64 b + 4 (2 w + blk) ..
+            const size_t base = ((size_t)64 * b + 4 * (2 * w + blk)) * kHeads * kRow;
+            for (int kt = 0; kt < 2; ++kt) kr[kt] = K + base + (size_t)(16 * kt + c16) * kRow + 16 * u;
+            for (int r = 0; r < 8; ++r) vr[r] = V + base + (size_t)(4 * r + u) * kRow + 16 * c16;
+        } else {
+            constexpr int chunk = 512 / HPW, rows = 8 / HPW, per_head = 8 / HPW;
+            const int row = b % rows, split = b / rows;
+            const int head = row * HPW + w % HPW;
+            const int key0 = chunk * split + 32 * (w / HPW + per_head * blk);
+            for (int kt = 0; kt < 2; ++kt)
+                kr[kt] = K + ((size_t)(key0 + 16 * kt + c16) * kHeads + head) * kRow + 16 * u;
+            for (int r = 0; r < 8; ++r)
+                vr[r] = V + ((size_t)(key0 + 4 * r + u) * kHeads + head) * kRow + 16 * c16;
+        }
+        for (int kt = 0; kt < 2; ++kt)
+            for (int t = 0; t < 4; ++t) kx[blk][4 * kt + t] = load16(kr[kt] + 64 * t);
+        for (int r = 0; r < 8; ++r) lds_dma16_nt(vr[r], &s_v[w][blk][0] + 512 * r);
+    }
+    // every load has landed before a loaded register is read
+    asm volatile("s_waitcnt vmcnt(0)"
+                 : "+v"(kx[0][0]), "+v"(kx[0][1]), "+v"(kx[0][2]), "+v"(kx[0][3]), "+v"(kx[0][4]),
+                   "+v"(kx[0][5]), "+v"(kx[0][6]), "+v"(kx[0][7]), "+v"(kx[1][0]), "+v"(kx[1][1]),
+                   "+v"(kx[1][2]), "+v"(kx[1][3]), "+v"(kx[1][4]), "+v"(kx[1][5]), "+v"(kx[1][6]),
+                   "+v"(kx[1][7])
+                 :
+                 : "memory");
+    __syncthreads();
+    unsigned x = s_v[w][0][lane] ^ s_v[w][1][lane];
+    for (int j = 0; j < 8; ++j) x ^= kx[0][j].x ^ kx[1][j].y;
+    if (lane == 0) out[b * 8 + w] = x;
+}
+
+__global__ void __launch_bounds__(256) stream_kernel(const uint8_t* K, const uint8_t* V, unsigned* out, int nwg) {
+    unsigned acc = 0;
+    const size_t n16 = kCache / 16, stride = (size_t)nwg * 256;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride) {
+        u32x4 x = load16(K + 16 * i), y = load16(V + 16 * i);
+        asm volatile("s_waitcnt vmcnt(0)" : "+v"(x), "+v"(y) : : "memory");
+        acc ^= x.x ^ y.z;
+    }
+    if (acc == 0x9e3779b9u) out[0] = acc;  // keeps the loads
+}
+
+template <class F>
+float time_layers(F launch) {
+    hipEvent_t e0, e1;
+    (void)hipEventCreate(&e0);
+    (void)hipEventCreate(&e1);
+    std::vector<float> t;
+    for (int rep = 0; rep < 7; ++rep) {
+        (void)hipEventRecord(e0);
+        for (int l = 0; l < kLayers; ++l) launch(l);
+        (void)hipEventRecord(e1);
+        (void)hipEventSynchronize(e1);
+        float ms = 0;
+        (void)hipEventElapsedTime(&ms, e0, e1);
+        t.push_back(ms * 1000.0f / kLayers);
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    std::sort(t.begin(), t.end());
+    return t[t.size() / 2];
+}
+
+}  // namespace
+
+int main() {
+    std::vector<uint8_t*> ks(kLayers), vs(kLayers);
+    for (int l = 0; l < kLayers; ++l) {
+        if (hipMalloc(&ks[l], kCache) != hipSuccess || hipMalloc(&vs[l], kCache) != hipSuccess) {
+            fprintf(stderr, "hipMalloc failed\n");
+            return 1;
+        }
+        (void)hipMemset(ks[l], 1, kCache);
+        (void)hipMemset(vs[l], 2, kCache);
+    }
+    unsigned* out = nullptr;
+    if (hipMalloc(&out, 256 * 8 * sizeof(unsigned)) != hipSuccess) return 1;
+    (void)hipDeviceSynchronize();
+    const double mb = 2.0 * kCache / 1e6;
+    auto line = [&](const char* name, float us) {
+        printf("| %s | %.2f | %.2f |\n", name, us, mb / us);  // MB per us = TB/s
+    };
+    printf("| pattern (%.1f MB per layer) | us per layer | TB/s |\n|---|---|---|\n", mb);
+    for (int pass = 0; pass < 2; ++pass) {
+        line("1 KV head per workgroup (the decode plan at 16K)",
+             time_layers([&](int l) { pattern_kernel<1><<<256, 512>>>(ks[l], vs[l], out); }));
+        line("2 KV heads per workgroup",
+             time_layers([&](int l) { pattern_kernel<2><<<256, 512>>>(ks[l], vs[l], out); }));
+        line("4 KV heads per workgroup",
+             time_layers([&](int l) { pattern_kernel<4><<<256, 512>>>(ks[l], vs[l], out); }));
+        line("whole 2 KB key rows",
+             time_layers([&](int l) { pattern_kernel<8><<<256, 512>>>(ks[l], vs[l], out); }));
+        for (int nwg : {512, 1024, 4096}) {
+            char name[64];
+            snprintf(name, sizeof name, "stream, %d workgroups of 256", nwg);
+            line(name, time_layers([&](int l) { stream_kernel<<<nwg, 256>>>(ks[l], vs[l], out, nwg); }));
+        }
+    }
+    const hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        fprintf(stderr, "%s\n", hipGetErrorString(e));
+        return 1;
+    }
+    return 0;
+}
