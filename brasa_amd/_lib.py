@@ -79,6 +79,10 @@ SYMBOLS = {
     "brasa_rt_event_record": (INT, [VP, VP]),
     "brasa_rt_event_elapsed_ms": (INT, [ctypes.POINTER(ctypes.c_float), VP, VP]),
     "brasa_rt_event_synchronize": (INT, [VP]),
+    "brasa_rt_stream_begin_capture": (INT, [VP]),
+    "brasa_rt_stream_end_capture": (INT, [VP, ctypes.POINTER(VP)]),
+    "brasa_rt_graph_launch": (INT, [VP, VP]),
+    "brasa_rt_graph_destroy": (INT, [VP]),
     "brasa_rt_mem_info": (INT, [ctypes.POINTER(SZ), ctypes.POINTER(SZ)]),
     "brasa_rt_fill_normal_f32": (INT, [VP, SZ, ctypes.c_uint64, ctypes.c_float, VP]),
 }

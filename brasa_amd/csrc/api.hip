@@ -421,6 +421,30 @@ int brasa_rt_event_elapsed_ms(float* ms, void* start, void* stop) {
 int brasa_rt_event_synchronize(void* event) {
     return hip_ok(hipEventSynchronize(static_cast<hipEvent_t>(event)), "hipEventSynchronize");
 }
+int brasa_rt_stream_begin_capture(void* stream) {
+    return hip_ok(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal),
+                  "hipStreamBeginCapture");
+}
+int brasa_rt_stream_end_capture(void* stream, void** graph_exec) {
+    *graph_exec = nullptr;
+    hipGraph_t g = nullptr;
+    int st = hip_ok(hipStreamEndCapture(as_stream(stream), &g), "hipStreamEndCapture");
+    if (st) return st;
+    hipGraphExec_t e = nullptr;
+    st = hip_ok(hipGraphInstantiate(&e, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+    const int st2 = hip_ok(hipGraphDestroy(g), "hipGraphDestroy");
+    if (st) return st;
+    *graph_exec = e;
+    return st2;
+}
+int brasa_rt_graph_launch(void* graph_exec, void* stream) {
+    return hip_ok(hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec), as_stream(stream)),
+                  "hipGraphLaunch");
+}
+int brasa_rt_graph_destroy(void* graph_exec) {
+    return hip_ok(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)),
+                  "hipGraphExecDestroy");
+}
 int brasa_rt_mem_info(size_t* free_bytes, size_t* total_bytes) {
     return hip_ok(hipMemGetInfo(free_bytes, total_bytes), "hipMemGetInfo");
 }

@@ -1674,11 +1674,27 @@ __device__ __forceinline__ f32x2 row_pair(const uint8_t* cache, size_t row, int 
 // holding dims 2 l, 2 l + 1; one key per step (the score is a wave sum). Slow, and free of any
 // f16 range limit on the cache values: the recompute of q8_0 calls whose f16(code * scale)
 // values leave the normal f16 range (it runs only when *gate == tag, i.e. after the fast launch
-// flagged such a scale; otherwise every wave exits at once).
+// flagged such a scale; otherwise every wave exits at once). A gated launch also clears the
+// flag once every workgroup has read it (the last to count itself in the word 8 past the flag
+// stores 0), so a graph replayed with the same tag starts each replay unflagged.
 template <int KV>
 __global__ void __launch_bounds__(256)
 prefill_exact_kernel(PrefillArgs a) {
-    if (a.gate && *a.gate != a.tag) return;
+    if (a.gate) {
+        __shared__ int s_go;
+        if (threadIdx.x == 0) {
+            const bool go = __hip_atomic_load(a.gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.tag;
+            if (go) {
+                const unsigned t = __builtin_amdgcn_atomic_inc32(a.taint + 8, gridDim.x - 1,
+                                                                 __ATOMIC_RELAXED, "agent");
+                if (t == gridDim.x - 1)
+                    __hip_atomic_store(a.taint, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            s_go = go;
+        }
+        __syncthreads();
+        if (!s_go) return;
+    }
     const int lane = threadIdx.x & 63;
     // query token * hq + query head, grid-stride (a small grid: the common launch only reads
     // the gate)
@@ -1822,7 +1838,7 @@ int launch_prec(PfCtx& c, PrefillArgs& a, int precision) {
                                : launch_q8_via_f16<HW>(c, a);
             if (st != BRASA_OK) return st;
             PrefillArgs g = a;
-            g.taint = nullptr;
+            g.taint = c.taint;  // cleared by the exact kernel (count at c.taint + 8)
             g.gate = c.taint;
             return launch_exact<KV>(c, g);
         }

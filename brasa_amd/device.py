@@ -6,6 +6,7 @@ one HIP runtime in the process.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 
 import numpy as np
@@ -96,6 +97,41 @@ class Stream:
         try:
             if self.handle:
                 lib().brasa_rt_stream_destroy(self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+
+class Graph:
+    """A HIP graph captured from the work one block enqueues on a stream:
+
+        with Graph.capture(stream) as g:
+            kernels.decode_attention_lanes(..., stream=stream)
+        g.launch(stream)   # replays the captured launches
+    """
+
+    def __init__(self):
+        self.handle = None
+
+    @classmethod
+    @contextlib.contextmanager
+    def capture(cls, stream: Stream):
+        g = cls()
+        check(lib().brasa_rt_stream_begin_capture(stream.handle))
+        try:
+            yield g
+        finally:
+            h = VP()
+            check(lib().brasa_rt_stream_end_capture(stream.handle, ctypes.byref(h)))
+            g.handle = h.value
+
+    def launch(self, stream: Stream) -> None:
+        check(lib().brasa_rt_graph_launch(self.handle, stream.handle))
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib().brasa_rt_graph_destroy(self.handle)
                 self.handle = None
         except Exception:
             pass

@@ -18,9 +18,13 @@
  *     on a device each get one, in the order they are first used; a launch on a stream without
  *     a slot uses a plan that needs no counters: one split per sequence in decode, no key split
  *     in prefill), the no-allocation decode array and the fixed prefill workspace (see
- *     brasa_flash_attention_with, brasa_release_workspaces). A graph captured from a stream
- *     keeps that stream's slot: do not replay it while other work on the same stream, or
- *     another replay of a graph captured there, is in flight.
+ *     brasa_flash_attention_with, brasa_release_workspaces). Every entry point can be captured
+ *     into a HIP graph (it enqueues kernels only: no allocation, no memset node, no host wait),
+ *     and a replay computes what an eager call on the replay's inputs computes, bit for bit
+ *     (the counters return to zero in every launch, the q8_0 range flag of prefill is cleared
+ *     by the launch that reads it). A graph captured from a stream keeps that stream's slot:
+ *     do not replay it while other work on the same stream, or another replay of a graph
+ *     captured there, is in flight.
  *   - Return value: BRASA_OK (0) or a BRASA_ERR_* code; brasa_last_error() then describes it
  *     (thread-local string, valid until the next call on the same thread).
  *

@@ -36,6 +36,17 @@ int brasa_rt_event_destroy(void* event);
 int brasa_rt_event_record(void* event, void* stream);
 int brasa_rt_event_elapsed_ms(float* ms, void* start, void* stop);
 int brasa_rt_event_synchronize(void* event);
+/*
+ * HIP graph capture of the work enqueued on `stream` (hipStreamCaptureModeThreadLocal):
+ * begin_capture starts it; end_capture ends it and returns an instantiated, launchable graph
+ * (hipGraphExec_t as void*); graph_launch enqueues a replay on `stream`; graph_destroy frees it.
+ * The attention entry points allocate nothing and record no memset node, so they can be
+ * captured (the conventions in brasa_attn.h say what a captured graph keeps).
+ */
+int brasa_rt_stream_begin_capture(void* stream);
+int brasa_rt_stream_end_capture(void* stream, void** graph_exec);
+int brasa_rt_graph_launch(void* graph_exec, void* stream);
+int brasa_rt_graph_destroy(void* graph_exec);
 /* Free and total device memory of the current device (hipMemGetInfo). */
 int brasa_rt_mem_info(size_t* free_bytes, size_t* total_bytes);
 

@@ -292,7 +292,11 @@ def test_flash_q8_equals_f16_on_dequantised_rows(tokens, pos0):
     f16(code * scale) and runs the f16 kernels: the same bits as F16 prefill over an f16 cache
     holding those values (rounded on the host from the oracle's exact dequantisation), at the
     threshold, a key-split chunk and T = 2048. (Smaller launches take the q8_0 kernel, checked
-    against the oracle by the other tests.)"""
+    against the oracle by the other tests.) The staging lives in the library's fixed workspace,
+    which the first stream that needs it owns: the test hands it back first, so that its calls
+    (on the default stream) own it whatever ran before."""
+    synchronize()
+    assert lib().brasa_release_workspaces() == 0
     k = Kernels()
     rng = oracle.Rng(97)
     lk = pos0 + tokens
