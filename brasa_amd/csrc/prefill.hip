@@ -61,10 +61,14 @@ struct PrefillArgs {
     unsigned* ctr;
     // q8_0 caches in F16 precision, whose values go through f16(code * scale): a launch that
     // meets a scale outside the range where that product is a normal f16 (see q8_f16_unsafe)
-    // stores `tag` at `taint`; the exact kernel launched after it runs only when *gate == tag
+    // stores `tag` at `taint`; the launch after it that holds gate = taint (the gated two-group
+    // f16 kernel, or prefill_exact_kernel) recomputes the call exactly only when *gate == tag
     unsigned* taint;
     const unsigned* gate;
     unsigned tag;
+    // q8_0 rows staged as f16: the cache itself, read by the exact path of a gated f16 launch
+    const uint8_t* k8;
+    const uint8_t* v8;
 };
 
 // True for the f16 scale bits of a q8_0 group whose f16(code * scale) products can leave the
@@ -74,6 +78,78 @@ struct PrefillArgs {
 __device__ __forceinline__ bool q8_f16_unsafe(uint32_t sc) {
     const uint32_t m = sc & 0x7fffu;
     return m >= 0x6008u || (m != 0 && m < 0x0400u);
+}
+
+
+// Two values d, d + 1 (d even) of cache row `row` as f32 (q8_0: code * scale, exact).
+template <int KV>
+__device__ __forceinline__ f32x2 row_pair(const uint8_t* cache, size_t row, int d) {
+    if constexpr (KV == BRASA_KV_F32) {
+        return *reinterpret_cast<const f32x2*>(cache + row * 512 + 4 * d);
+    } else if constexpr (KV == BRASA_KV_F16) {
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(cache + row * 256 + 2 * d);
+        return f32x2{h2f((uint16_t)(w & 0xffffu)), h2f((uint16_t)(w >> 16))};
+    } else {
+        const uint8_t* r = cache + row * kQ8Row;
+        const uint16_t c = *reinterpret_cast<const uint16_t*>(r + d);
+        const float sc = h2f(*reinterpret_cast<const uint16_t*>(r + 128 + 2 * (d >> 5)));
+        return f32x2{(float)(int8_t)(c & 0xffu) * sc, (float)(int8_t)(c >> 8) * sc};
+    }
+}
+
+// Exact F16 prefill in plain f32 arithmetic, the reference F16 kernel's numerics
+// (flash_attention.metal:152-323: Q * scale rounded to f16, K / V as exact f32 values, scores,
+// softmax, P and O in f32, o rounded to f16): query row rw = token * hq + head of the cache
+// (k, v), computed by one wave, lane l holding dims 2 l, 2 l + 1, one key per step (the score
+// is a wave sum). Slow, and free of any f16 range limit on the cache values.
+template <int KV>
+__device__ __forceinline__ void exact_row(const PrefillArgs& a, const uint8_t* k, const uint8_t* v,
+                                          int rw, int lane) {
+    const int t = rw / a.hq, h = rw - t * a.hq, kh = h / a.group, d = 2 * lane;
+    const f32x2 qv = *reinterpret_cast<const f32x2*>(a.q + (size_t)rw * kDim + d);
+    const float q0 = h2f(f2h(as_f32(qv.x * a.scale))), q1 = h2f(f2h(as_f32(qv.y * a.scale)));
+    float m = -INFINITY, l = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    const int kend = a.pos0 + t + 1;
+    for (int j = 0; j < kend; ++j) {
+        const size_t row = (size_t)j * a.hkv + kh;
+        const f32x2 kk = row_pair<KV>(k, row, d);
+        const f32x2 vv = row_pair<KV>(v, row, d);
+        float sc = row16_sum(fmaf(q0, kk.x, q1 * kk.y));
+        sc += __shfl_xor(sc, 16, 64);
+        sc += __shfl_xor(sc, 32, 64);
+        const float x = sc * kLog2e;
+        const float mn = fmaxf(m, x);
+        const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+        const float p = __builtin_amdgcn_exp2f(x - mn);
+        l = fmaf(l, alpha, p);
+        o0 = fmaf(o0, alpha, p * vv.x);
+        o1 = fmaf(o1, alpha, p * vv.y);
+        m = mn;
+    }
+    const float inv = 1.0f / l;
+    *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.o) + (size_t)rw * kDim + d) =
+        (uint32_t)f2h(o0 * inv) | ((uint32_t)f2h(o1 * inv) << 16);
+}
+
+// The range gate of a q8_0 F16 call (every thread of the workgroup calls it): true when the
+// launch before this one flagged a scale (*gate == tag). A workgroup that finds it set counts
+// itself in the word 8 past the flag; the last of the grid stores 0 there, so the flag is
+// cleared once every workgroup has read it, and a graph replayed with the same tag starts each
+// replay unflagged.
+__device__ __forceinline__ bool gate_open(const PrefillArgs& a) {
+    __shared__ int s_go;
+    if (threadIdx.x == 0) {
+        const bool go = __hip_atomic_load(a.gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.tag;
+        if (go) {
+            const unsigned n = gridDim.x * gridDim.y;
+            const unsigned t = __builtin_amdgcn_atomic_inc32(a.taint + 8, n - 1, __ATOMIC_RELAXED,
+                                                             "agent");
+            if (t == n - 1) __hip_atomic_store(a.taint, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        s_go = go;
+    }
+    __syncthreads();
+    return s_go;
 }
 
 
@@ -917,10 +993,37 @@ __device__ __forceinline__ void f16_pp_tile(const PrefillArgs& a, const int tile
 // a.pair the workgroup for y also takes the light tile y after the heavy tile ntiles - 1 - y, so
 // each CU receives a pair of equal total work in one round (without it, a CU that finishes a
 // light tile early takes the next one).
-template <int HW, bool PS>
+// GATED (q8_0 rows staged as f16 in F16 precision): the workgroup first reads the range gate
+// of the call (gate_open); when the staging flagged a scale, it computes its query tiles with the
+// exact path from the q8_0 cache (a.k8, a.v8) instead (the tile's key part 0 does, the other
+// parts return), so such calls need no separate exact launch.
+template <int HW, bool PS, bool GATED = false>
 __global__ void __launch_bounds__(2 * kThreads, 1)
 prefill_f16_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t s_kv[2][2][2][kStageHalves];
+    if constexpr (GATED) {
+        if (gate_open(a)) {
+            constexpr int TPW = 32 * 4 / HW;
+            const int y = blockIdx.y;
+            int tiles[2] = {-1, -1};
+            if (a.kparts > 1) {
+                if (y % a.kparts == 0) tiles[0] = a.ntiles - 1 - y / a.kparts;
+            } else {
+                tiles[0] = a.ntiles - 1 - y;
+                if (a.pair && y < tiles[0]) tiles[1] = y;
+            }
+            const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+            for (int ti = 0; ti < 2; ++ti) {
+                if (tiles[ti] < 0) continue;
+                const int t0 = tiles[ti] * TPW, nt = min(TPW, a.tokens - t0);
+                // rows (token t0 + i, head blockIdx.x * HW + j), one per wave at a time
+                for (int r = wave; r < nt * HW; r += 2 * kThreads / 64)
+                    exact_row<BRASA_KV_Q8_0>(a, a.k8, a.v8,
+                                             (t0 + r / HW) * a.hq + blockIdx.x * HW + r % HW, lane);
+            }
+            return;
+        }
+    }
     PREFILL_STAMP(0);
     u32x4 qraw[8];
     if (a.kparts > 1) {  // workgroup y: key part y % kparts of query tile ntiles - 1 - y / kparts
@@ -1652,78 +1755,19 @@ dequant_q8_f16_kernel(const uint8_t* k, const uint8_t* v, uint16_t* kd, uint16_t
     out[1] = u32x4{w[4], w[5], w[6], w[7]};
 }
 
-// Two values d, d + 1 (d even) of cache row `row` as f32 (q8_0: code * scale, exact).
-template <int KV>
-__device__ __forceinline__ f32x2 row_pair(const uint8_t* cache, size_t row, int d) {
-    if constexpr (KV == BRASA_KV_F32) {
-        return *reinterpret_cast<const f32x2*>(cache + row * 512 + 4 * d);
-    } else if constexpr (KV == BRASA_KV_F16) {
-        const uint32_t w = *reinterpret_cast<const uint32_t*>(cache + row * 256 + 2 * d);
-        return f32x2{h2f((uint16_t)(w & 0xffffu)), h2f((uint16_t)(w >> 16))};
-    } else {
-        const uint8_t* r = cache + row * kQ8Row;
-        const uint16_t c = *reinterpret_cast<const uint16_t*>(r + d);
-        const float sc = h2f(*reinterpret_cast<const uint16_t*>(r + 128 + 2 * (d >> 5)));
-        return f32x2{(float)(int8_t)(c & 0xffu) * sc, (float)(int8_t)(c >> 8) * sc};
-    }
-}
-
-// Exact F16 prefill in plain f32 arithmetic, the reference F16 kernel's numerics
-// (flash_attention.metal:152-323: Q * scale rounded to f16, K / V as exact f32 values, scores,
-// softmax, P and O in f32, o rounded to f16). One wave per (query token, query head), lane l
-// holding dims 2 l, 2 l + 1; one key per step (the score is a wave sum). Slow, and free of any
-// f16 range limit on the cache values: the recompute of q8_0 calls whose f16(code * scale)
-// values leave the normal f16 range (it runs only when *gate == tag, i.e. after the fast launch
-// flagged such a scale; otherwise every wave exits at once). A gated launch also clears the
-// flag once every workgroup has read it (the last to count itself in the word 8 past the flag
-// stores 0), so a graph replayed with the same tag starts each replay unflagged.
+// The recompute of q8_0 calls whose f16(code * scale) values leave the normal f16 range, for the
+// launches whose fast kernel has no gate of its own (prefill_q8_kernel4, the four-wave f16
+// kernels): it runs only when *gate == tag, i.e. after the fast launch flagged such a scale;
+// otherwise every wave exits at once.
 template <int KV>
 __global__ void __launch_bounds__(256)
 prefill_exact_kernel(PrefillArgs a) {
-    if (a.gate) {
-        __shared__ int s_go;
-        if (threadIdx.x == 0) {
-            const bool go = __hip_atomic_load(a.gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.tag;
-            if (go) {
-                const unsigned t = __builtin_amdgcn_atomic_inc32(a.taint + 8, gridDim.x - 1,
-                                                                 __ATOMIC_RELAXED, "agent");
-                if (t == gridDim.x - 1)
-                    __hip_atomic_store(a.taint, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            s_go = go;
-        }
-        __syncthreads();
-        if (!s_go) return;
-    }
+    if (a.gate && !gate_open(a)) return;
     const int lane = threadIdx.x & 63;
     // query token * hq + query head, grid-stride (a small grid: the common launch only reads
     // the gate)
-    for (int rw = blockIdx.x * 4 + (threadIdx.x >> 6); rw < a.tokens * a.hq; rw += gridDim.x * 4) {
-        const int t = rw / a.hq, h = rw - t * a.hq, kh = h / a.group, d = 2 * lane;
-        const f32x2 qv = *reinterpret_cast<const f32x2*>(a.q + (size_t)rw * kDim + d);
-        const float q0 = h2f(f2h(as_f32(qv.x * a.scale))), q1 = h2f(f2h(as_f32(qv.y * a.scale)));
-        float m = -INFINITY, l = 0.0f, o0 = 0.0f, o1 = 0.0f;
-        const int kend = a.pos0 + t + 1;
-        for (int j = 0; j < kend; ++j) {
-            const size_t row = (size_t)j * a.hkv + kh;
-            const f32x2 kk = row_pair<KV>(a.k, row, d);
-            const f32x2 vv = row_pair<KV>(a.v, row, d);
-            float sc = row16_sum(fmaf(q0, kk.x, q1 * kk.y));
-            sc += __shfl_xor(sc, 16, 64);
-            sc += __shfl_xor(sc, 32, 64);
-            const float x = sc * kLog2e;
-            const float mn = fmaxf(m, x);
-            const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
-            const float p = __builtin_amdgcn_exp2f(x - mn);
-            l = fmaf(l, alpha, p);
-            o0 = fmaf(o0, alpha, p * vv.x);
-            o1 = fmaf(o1, alpha, p * vv.y);
-            m = mn;
-        }
-        const float inv = 1.0f / l;
-        *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.o) + (size_t)rw * kDim + d) =
-            (uint32_t)f2h(o0 * inv) | ((uint32_t)f2h(o1 * inv) << 16);
-    }
+    for (int rw = blockIdx.x * 4 + (threadIdx.x >> 6); rw < a.tokens * a.hq; rw += gridDim.x * 4)
+        exact_row<KV>(a, a.k, a.v, rw, lane);
 }
 
 template <int KV>
@@ -1743,25 +1787,28 @@ int launch(PfCtx& c, const PrefillArgs& a) {
     return check_launch("prefill_kernel");
 }
 
-template <int HW, bool PS>
-int launch_f16(PfCtx& c, const PrefillArgs& a) {
+// GATED: a q8_0 F16 launch on staged f16 rows (a.gate set); *gated is set when the kernel
+// launched reads the gate itself (the two-group kernel), so the caller needs no exact launch.
+template <int HW, bool PS, bool GATED = false>
+int launch_f16(PfCtx& c, const PrefillArgs& a, bool* gated = nullptr) {
     const long long wgs = (long long)(a.hq / HW) * a.ntiles;
     const int variant = g_force_variant.load(std::memory_order_relaxed);
     const int pick = variant ? variant : wgs <= 2 * 256 ? 1 : wgs < 3 * 256 ? 2 : 4;
     if (pick == 1) {
+        if (gated) *gated = GATED;
         PrefillArgs b = a;
         b.pair = g_allow_pair.load(std::memory_order_relaxed) && wgs >= 2 * 256;
         // one workgroup per CU
         const int parts = clamp_parts(variant ? g_force_parts.load(std::memory_order_relaxed)
                                               : key_parts(wgs, a.pos0 + a.tokens, 256), wgs);
         if (parts > 1) {
-            const int st = launch_split(c, prefill_f16_kernel<HW, PS>, "prefill_f16_kernel", b, HW,
-                                        wgs, parts, 2 * kThreads);
+            const int st = launch_split(c, prefill_f16_kernel<HW, PS, GATED>, "prefill_f16_kernel",
+                                        b, HW, wgs, parts, 2 * kThreads);
             if (st != 1) return st;
         }
         if (c.measure) return BRASA_OK;
         const int rows = b.pair ? (a.ntiles + 1) / 2 : a.ntiles;
-        hipLaunchKernelGGL((prefill_f16_kernel<HW, PS>), dim3(a.hq / HW, rows),
+        hipLaunchKernelGGL((prefill_f16_kernel<HW, PS, GATED>), dim3(a.hq / HW, rows),
                            dim3(2 * kThreads), 0, c.stream, b);
         return check_launch("prefill_f16_kernel");
     }
@@ -1798,7 +1845,7 @@ int launch_q8_kernel4(PfCtx& c, const PrefillArgs& a) {
 // values are those prefill_q8_kernel4 computes in registers, f16(code * scale), and the f16
 // kernels' tile schedule is the faster one. Without room for the staging: prefill_q8_kernel4.
 template <int HW>
-int launch_q8_via_f16(PfCtx& c, const PrefillArgs& a) {
+int launch_q8_via_f16(PfCtx& c, const PrefillArgs& a, bool* gated) {
     const long long rows = (long long)((a.pos0 + a.tokens + 63) / 64 * 64) * a.hkv;
     const size_t bytes = (size_t)rows * kDim * 2;
     void* ws = c.take(2 * bytes);
@@ -1814,7 +1861,10 @@ int launch_q8_via_f16(PfCtx& c, const PrefillArgs& a) {
     PrefillArgs b = a;
     b.k = reinterpret_cast<const uint8_t*>(kd);
     b.v = reinterpret_cast<const uint8_t*>(vd);
-    return launch_f16<HW, false>(c, b);
+    b.k8 = a.k;
+    b.v8 = a.v;
+    b.gate = a.taint;  // flagged by the staging launch above; read (and cleared) by the f16 launch
+    return launch_f16<HW, false, true>(c, b, gated);
 }
 
 template <int KV, int HW>
@@ -1828,15 +1878,17 @@ int launch_prec(PfCtx& c, PrefillArgs& a, int precision) {
             // the f16 kernels on dequantised rows when the work is large enough to hide the
             // dequantisation launch (measured: T = 384 at pos0 0 is the crossover; 128 tokens
             // after 16384 cached positions already gain 81 -> 71 us), else the q8_0 kernel.
-            // Both flag scales whose f16(code * scale) can leave the normal f16 range; the exact
-            // kernel (the reference's F16 numerics in f32) then recomputes the call, and
+            // Both flag scales whose f16(code * scale) can leave the normal f16 range; the next
+            // launch then recomputes the call exactly (the reference's F16 numerics in f32):
+            // the gated two-group f16 kernel itself, or else prefill_exact_kernel, which
             // otherwise exits at once.
             a.taint = c.taint;
             a.tag = c.tag;
+            bool gated = false;
             const int st = (long long)a.tokens * (a.pos0 + a.tokens) < 384LL * 384
                                ? launch_q8_kernel4<HW>(c, a)
-                               : launch_q8_via_f16<HW>(c, a);
-            if (st != BRASA_OK) return st;
+                               : launch_q8_via_f16<HW>(c, a, &gated);
+            if (st != BRASA_OK || gated) return st;
             PrefillArgs g = a;
             g.taint = c.taint;  // cleared by the exact kernel (count at c.taint + 8)
             g.gate = c.taint;
@@ -1884,6 +1936,8 @@ PrefillArgs make_args(const float* q, const void* k, const void* v, void* o, int
     a.taint = nullptr;
     a.gate = nullptr;
     a.tag = 0;
+    a.k8 = nullptr;
+    a.v8 = nullptr;
     a.scale = 1.0f / sqrtf(static_cast<float>(kDim));
     return a;
 }

@@ -210,8 +210,9 @@ int brasa_decode_attention_batch(const float* q, const void* const* k, const voi
  * dequantised to f16 (each value f16(code * scale)) into the workspace (512 B per row of K and
  * V), and the f16 kernels run on it; small calls convert the same values in registers. When a
  * group scale lets f16(code * scale) leave the normal f16 range (|scale| >= 516, f16-subnormal,
- * inf or NaN scales) the call is recomputed by the exact kernel (the reference's F16 numerics:
- * Q rounded to f16, K / V exact, P f32), which costs one more short launch on every such call.
+ * inf or NaN scales) the call is recomputed exactly (the reference's F16 numerics: Q rounded
+ * to f16, K / V exact, P f32) by the launch after the conversion, which reads a flag the
+ * conversion sets (on some plans a separate short launch on every q8_0 F16 call).
  * Like the reference's, this call allocates nothing: its workspace is a fixed 96 MiB device
  * array of the library, owned by the first stream that needs it (until
  * brasa_release_workspaces); calls on other streams, or whose plan needs more, run without the
