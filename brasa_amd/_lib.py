@@ -56,7 +56,8 @@ SYMBOLS = {
     "brasa_rope_neox": (INT, [VP, RopeTableC, SZ, SZ, SZ, SZ, VP]),
     "brasa_qk_norm_rope_store": (INT, [INT, VP, VP, VP, VP, VP, ctypes.c_float, RopeTableC, VP,
                                        VP, AttnShapeC, VP]),
-    "brasa_test_set_prefill_layout": (INT, [INT, INT, INT]),
+    "brasa_test_flash_attention_layout": (INT, [VP, VP, VP, VP, AttnShapeC, INT, INT, INT, INT,
+                                                VP]),
     "brasa_test_stream_slot": (INT, [INT, VP, ctypes.POINTER(INT)]),
     "brasa_release_workspaces": (INT, []),
     "brasa_last_error": (ctypes.c_char_p, []),

@@ -33,10 +33,9 @@ int decode_batch_launch(const float* q, const void* const* k, const void* const*
                         int hkv, int kv, bool per_head, hipStream_t stream);
 int prefill_launch(const float* q, const void* k, const void* v, void* o, int tokens, int hq,
                    int hkv, int pos0, int kv, int precision, bool caller_ws, void* ws,
-                   size_t ws_len, hipStream_t stream);
+                   size_t ws_len, hipStream_t stream, const int* layout = nullptr);
 size_t prefill_workspace_len(int tokens, int hq, int hkv, int pos0, int kv, int precision);
 void prefill_release_workspaces();
-void prefill_set_layout(int variant, int pair, int parts);
 
 namespace {
 thread_local char g_err[512] = "";
@@ -342,14 +341,21 @@ int brasa_release_workspaces(void) {
     return BRASA_OK;
 }
 
-int brasa_test_set_prefill_layout(int variant, int pair, int parts) {
+int brasa_test_flash_attention_layout(const float* q, const void* k, const void* v, void* o,
+                                      brasa_attn_shape s, int precision, int variant, int pair,
+                                      int parts, void* stream) {
     g_err[0] = 0;
     if (variant != 0 && variant != 1 && variant != 2 && variant != 4)
         return set_error(BRASA_ERR_ARG, "prefill layout: variant %d (0, 1, 2 or 4)", variant);
     if (parts < 1 || parts > 8)
         return set_error(BRASA_ERR_ARG, "prefill layout: %d key parts (1 .. 8)", parts);
-    prefill_set_layout(variant, pair ? 1 : 0, parts);
-    return BRASA_OK;
+    const int st = prefill_check(s, precision);
+    if (st != BRASA_OK) return st;
+    if (s.tokens == 0) return BRASA_OK;
+    if (!q || !k || !v || !o) return set_error(BRASA_ERR_ARG, "flash_attention: null pointer");
+    const int layout[3] = {variant, pair ? 1 : 0, parts};
+    return prefill_launch(q, k, v, o, (int)s.tokens, (int)s.hq, (int)s.hkv, (int)s.pos0, s.kv,
+                          precision, false, nullptr, 0, as_stream(stream), layout);
 }
 
 const char* brasa_last_error(void) { return g_err; }

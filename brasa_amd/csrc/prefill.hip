@@ -1633,11 +1633,9 @@ prefill_f16_kernel4s(PrefillArgs a) {
 // CU (T = 4096: 156 vs 187 µs; T = 8192: 580 vs 631 µs); in between the four-wave kernel
 // (T = 2560: 76 vs 82 µs). The two-group kernel pairs heavy and light query tiles when the pairs
 // still fill every CU (T = 2048: 57.0 vs 58.6 µs; at T = 1536 the 192 pairs leave CUs idle,
-// 44 vs 39 µs). brasa_test_set_prefill_layout() forces a kernel or turns pairing off, for tests
-// that cover every kernel at small sizes; the product path never calls it.
-std::atomic<int> g_force_variant{0};  // 0: chosen by size; 1, 2, 4: the kernels above
-std::atomic<int> g_allow_pair{1};
-std::atomic<int> g_force_parts{1};    // key parts of a forced prefill_f16_kernel launch
+// 44 vs 39 µs). The test entry point brasa_test_flash_attention_layout() forces a kernel, turns
+// pairing off or sets the key split for one call (PfCtx::variant / pair / parts), so tests cover
+// every kernel at small sizes; the reference-signature entry points keep the choice by size.
 
 
 // Arrival counters of the key-split merge: one per (query tile, wave), 64 bytes apart; a slot
@@ -1677,6 +1675,12 @@ struct PfCtx {
     unsigned* ctr = nullptr;
     unsigned* taint = nullptr;
     unsigned tag = 0;
+    // layout of this call: variant 0 chooses the f16 kernel by size, 1 / 2 / 4 force one (the
+    // two-group kernel, four waves, four waves on 32-key stages); pair 0 keeps the two-group
+    // kernel from pairing query tiles; parts: key parts of a forced two-group launch
+    int variant = 0;
+    int pair = 1;
+    int parts = 1;
 
     void* take(size_t bytes) {
         bytes = (bytes + 255) / 256 * 256;
@@ -1792,15 +1796,15 @@ int launch(PfCtx& c, const PrefillArgs& a) {
 template <int HW, bool PS, bool GATED = false>
 int launch_f16(PfCtx& c, const PrefillArgs& a, bool* gated = nullptr) {
     const long long wgs = (long long)(a.hq / HW) * a.ntiles;
-    const int variant = g_force_variant.load(std::memory_order_relaxed);
+    const int variant = c.variant;
     const int pick = variant ? variant : wgs <= 2 * 256 ? 1 : wgs < 3 * 256 ? 2 : 4;
     if (pick == 1) {
         if (gated) *gated = GATED;
         PrefillArgs b = a;
-        b.pair = g_allow_pair.load(std::memory_order_relaxed) && wgs >= 2 * 256;
+        b.pair = c.pair && wgs >= 2 * 256;
         // one workgroup per CU
-        const int parts = clamp_parts(variant ? g_force_parts.load(std::memory_order_relaxed)
-                                              : key_parts(wgs, a.pos0 + a.tokens, 256), wgs);
+        const int parts = clamp_parts(variant ? c.parts : key_parts(wgs, a.pos0 + a.tokens, 256),
+                                      wgs);
         if (parts > 1) {
             const int st = launch_split(c, prefill_f16_kernel<HW, PS, GATED>, "prefill_f16_kernel",
                                         b, HW, wgs, parts, 2 * kThreads);
@@ -1957,11 +1961,6 @@ void prefill_release_workspaces() {
     for (auto& o : g_pf_static_owner) o.store(0, std::memory_order_relaxed);
 }
 
-void prefill_set_layout(int variant, int pair, int parts) {
-    g_force_variant.store(variant, std::memory_order_relaxed);
-    g_allow_pair.store(pair, std::memory_order_relaxed);
-    g_force_parts.store(parts, std::memory_order_relaxed);
-}
 
 size_t prefill_workspace_len(int tokens, int hq, int hkv, int pos0, int kv, int precision) {
     PrefillArgs a = make_args(nullptr, nullptr, nullptr, nullptr, tokens, hq, hkv, pos0);
@@ -1976,7 +1975,7 @@ size_t prefill_workspace_len(int tokens, int hq, int hkv, int pos0, int kv, int 
 // the reference-signature call (the fixed workspace when this stream owns it).
 int prefill_launch(const float* q, const void* k, const void* v, void* o, int tokens, int hq,
                    int hkv, int pos0, int kv, int precision, bool caller_ws, void* ws,
-                   size_t ws_len, hipStream_t stream) {
+                   size_t ws_len, hipStream_t stream, const int* layout) {
     int dev = 0, slot = -1;
     int st = stream_slot(stream, &dev, &slot);
     if (st != BRASA_OK) return st;
@@ -1992,6 +1991,11 @@ int prefill_launch(const float* q, const void* k, const void* v, void* o, int to
         return set_error(BRASA_ERR_LAUNCH, "flash_attention: arrival counters not found");
     PfCtx c;
     c.stream = stream;
+    if (layout) {
+        c.variant = layout[0];
+        c.pair = layout[1];
+        c.parts = layout[2];
+    }
     if (slot >= 0) {
         c.ctr = g_pf_ctr_base[dev] + (size_t)slot * kPfSlotWords;
         c.taint = g_pf_taint_base[dev] + (size_t)slot * 16;

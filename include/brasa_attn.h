@@ -305,16 +305,19 @@ int brasa_qk_norm_rope_store(int kv, float* q, float* k, const float* v, const f
 int brasa_release_workspaces(void);
 
 /*
- * Test hook (no counterpart in the reference; a production caller never needs it). The prefill
- * kernel for BRASA_KV_F16 is chosen by workgroup count; tests force each of the three kernels at
- * small sizes with variant 1 (two key groups per workgroup), 2 (four waves) or 4 (four waves,
- * 32-key stages), and 0 restores the choice by size. pair = 0 stops the two-group kernel from
- * pairing heavy and light query tiles (the results are identical either way). parts (1 .. 8)
- * is the number of workgroups each query tile's keys are split over when variant 1 is forced
- * (with variant 0 the split is chosen by size: short chunks after long prefixes). Process-wide;
- * set it only while no prefill call is being enqueued on another thread.
+ * Test entry point (no counterpart in the reference; a production caller never needs it):
+ * brasa_flash_attention_with with the prefill layout of this one call forced. The kernel for
+ * BRASA_KV_F16 (and for q8_0 rows staged as f16) is otherwise chosen by workgroup count; tests
+ * cover each of the three kernels at small sizes with variant 1 (two key groups per workgroup),
+ * 2 (four waves) or 4 (four waves, 32-key stages); 0 keeps the choice by size. pair = 0 stops
+ * the two-group kernel from pairing heavy and light query tiles (the results are identical
+ * either way). parts (1 .. 8) is the number of workgroups each query tile's keys are split over
+ * when variant 1 is forced (with variant 0 the split is chosen by size). Nothing outlives the
+ * call: there is no process-wide layout state.
  */
-int brasa_test_set_prefill_layout(int variant, int pair, int parts);
+int brasa_test_flash_attention_layout(const float* q, const void* k, const void* v, void* o,
+                                      brasa_attn_shape shape, int precision, int variant,
+                                      int pair, int parts, void* stream);
 
 /*
  * Test hook (no counterpart in the reference). The counter slot of `stream` on `device` that the

@@ -220,12 +220,16 @@ def test_decode_batch_asserts_without_device():
     k.decode_attention_batch(fake, [], [], [], Part, fake, 32, 8, KvType.F16)
 
 
-def test_prefill_layout_hook_validates():
+def test_prefill_layout_entry_validates():
+    """The per-call layout of brasa_test_flash_attention_layout is checked before anything is
+    enqueued (no GPU needed: the errors come first)."""
+    from brasa_amd import AttnShape, KvType, PrefillPrecision
     from brasa_amd._lib import BrasaError, check
+    shape = AttnShape(64, 32, 8, 128, 0, KvType.F16).c()
     for bad in [(3, 1, 1), (1, 1, 0), (1, 1, 9)]:
         with pytest.raises(BrasaError):
-            check(lib().brasa_test_set_prefill_layout(*bad))
-    check(lib().brasa_test_set_prefill_layout(0, 1, 1))
+            check(lib().brasa_test_flash_attention_layout(1, 1, 1, 1, shape,
+                                                          int(PrefillPrecision.F16), *bad, None))
 
 
 def test_stream_slots():

@@ -37,6 +37,19 @@ def _say(msg):
     print(msg, flush=True)
 
 
+def run_prefill_layout(q, cache, tokens, hq, hkv, pos0, precision, variant, pair, parts):
+    """run_prefill through brasa_test_flash_attention_layout: the kernel, the tile pairing and
+    the key split of this call forced."""
+    gq = DeviceBuffer.from_array(q)
+    o = DeviceBuffer(tokens * hq * DIM * 2)
+    check(lib().brasa_test_flash_attention_layout(
+        gq.ptr, cache.kbuf.ptr, cache.vbuf.ptr, o.ptr,
+        AttnShape(tokens, hq, hkv, DIM, pos0, cache.kv).c(), int(precision), variant, pair,
+        parts, None))
+    synchronize()
+    return o.download(np.uint16).reshape(tokens, hq, DIM)
+
+
 def run_prefill(k, q, cache, tokens, hq, hkv, pos0, precision):
     gq = DeviceBuffer.from_array(q)
     f32 = precision == PrefillPrecision.F32
@@ -187,17 +200,12 @@ def test_flash_paired_tiles():
     cap = (lk + 63) // 64 * 64
     q = rng.vec(tokens * hq * DIM, 2.0)
     cache = KvPair(KvType.F16, rng.vec(cap * hkv * DIM, 2.0), rng.vec(cap * hkv * DIM, 3.0))
-    try:
-        check(lib().brasa_test_set_prefill_layout(1, 1, 1))
-        _say(f"prefill paired F16 hq={hq} T={tokens} pos0={pos0}")
-        oh = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
-        _say(f"prefill paired F16_PF32 hq={hq} T={tokens} pos0={pos0}")
-        op = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16_PF32)
-        check(lib().brasa_test_set_prefill_layout(1, 0, 1))
-        _say(f"prefill unpaired F16 hq={hq} T={tokens} pos0={pos0}")
-        ou = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
-    finally:
-        check(lib().brasa_test_set_prefill_layout(0, 1, 1))
+    _say(f"prefill paired F16 hq={hq} T={tokens} pos0={pos0}")
+    oh = run_prefill_layout(q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16, 1, 1, 1)
+    _say(f"prefill paired F16_PF32 hq={hq} T={tokens} pos0={pos0}")
+    op = run_prefill_layout(q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16_PF32, 1, 1, 1)
+    _say(f"prefill unpaired F16 hq={hq} T={tokens} pos0={pos0}")
+    ou = run_prefill_layout(q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16, 1, 0, 1)
     assert np.array_equal(oh, ou)
     for t0, t1 in [(0, 32), (512, 544), (1024, 1040)]:
         ref16, vmax = oracle.attention(q, cache.k, cache.v, tokens, hq, hkv, DIM, pos0,
@@ -223,18 +231,14 @@ def test_flash_key_split(parts):
     cap = (lk + 63) // 64 * 64
     q = rng.vec(tokens * hq * DIM, 2.0)
     cache = KvPair(KvType.F16, rng.vec(cap * hkv * DIM, 2.0), rng.vec(cap * hkv * DIM, 3.0))
-    try:
-        check(lib().brasa_test_set_prefill_layout(1, 0, parts))
-        _say(f"prefill key split parts={parts} F16 T={tokens} pos0={pos0}")
-        oh = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
-        _say(f"prefill key split parts={parts} F16_PF32 T={tokens} pos0={pos0}")
-        op = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16_PF32)
-        oh2 = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
-        check(lib().brasa_test_set_prefill_layout(1, 0, 1))
-        _say(f"prefill unsplit F16 T={tokens} pos0={pos0}")
-        o1 = run_prefill(k, q, cache, tokens, hq, hkv, pos0, PrefillPrecision.F16)
-    finally:
-        check(lib().brasa_test_set_prefill_layout(0, 1, 1))
+    F16, PF32 = PrefillPrecision.F16, PrefillPrecision.F16_PF32
+    _say(f"prefill key split parts={parts} F16 T={tokens} pos0={pos0}")
+    oh = run_prefill_layout(q, cache, tokens, hq, hkv, pos0, F16, 1, 0, parts)
+    _say(f"prefill key split parts={parts} F16_PF32 T={tokens} pos0={pos0}")
+    op = run_prefill_layout(q, cache, tokens, hq, hkv, pos0, PF32, 1, 0, parts)
+    oh2 = run_prefill_layout(q, cache, tokens, hq, hkv, pos0, F16, 1, 0, parts)
+    _say(f"prefill unsplit F16 T={tokens} pos0={pos0}")
+    o1 = run_prefill_layout(q, cache, tokens, hq, hkv, pos0, F16, 1, 0, 1)
     assert np.array_equal(oh, oh2)  # the merge order is fixed: repeat calls give equal bits
     ref16, vmax = oracle.attention(q, cache.k, cache.v, tokens, hq, hkv, DIM, pos0, q16=True)
     a, r = bars(oracle.f16_to_f32(oh), ref16)
