@@ -643,8 +643,9 @@ decode_f32_kernel(DecodeArgs<NS> a) {
 // ones pending. The wait names the registers it guards as operands, so no use of them can be
 // scheduled above it. Block i + kRing is issued into block i's ring slot once block i has been
 // computed.
-// Softmax: columns c < G hold the hi halves of the split Q / P operands, G <= c < 2 G the lo
-// halves; one DPP exchange adds them (the same bits in both lanes). The running max is lazy: the
+// Softmax: columns c < G hold the hi halves of the split Q / P operands, the partner columns
+// (col_is_lo) the lo halves; one DPP exchange adds them (the same bits in both lanes). Only the
+// split's last block masks keys past its end. The running max is lazy: the
 // reference point moves only when a block's max exceeds it by more than 2^8, so most blocks skip
 // the rescale of O.
 constexpr int kRing = 2;                    // blocks in flight per wave (16 instructions each)
@@ -673,15 +674,25 @@ __device__ __forceinline__ void wait_k(u32x4 (&k)[8]) {
                  : "n"(N)
                  : "memory");
 }
-// value of lane (lane ^ M) of the same 16-lane row, M in {1, 2, 4, 8}, through DPP
-template <int M>
-__device__ __forceinline__ float xor_row(float x, int c16) {
-    if constexpr (M == 1) return dpp<0xB1>(x);  // quad_perm [1, 0, 3, 2]
-    if constexpr (M == 2) return dpp<0x4E>(x);  // quad_perm [2, 3, 0, 1]
-    if constexpr (M == 8) return dpp<0x128>(x); // row_ror:8
-    // M == 4: lanes with bit 2 clear read lane + 4 (row_ror:12), the others lane - 4 (row_ror:4)
-    const float up = dpp<0x12C>(x), down = dpp<0x124>(x);
-    return (c16 & 4) ? down : up;
+// Columns of the S^T / P^T MFMA operands of the f16 and q8_0 kernels for G query heads: head c
+// (c < G) in column c with the hi half of its Q / P split, and its lo half in the partner column:
+// 7 - c for G <= 4, so one row_half_mirror DPP exchanges the two halves, c + 8 for G = 8
+// (row_ror:8). The other columns are zero.
+template <int G>
+__device__ __forceinline__ bool col_is_lo(int c16) {
+    if constexpr (G == 8) return c16 >= 8;
+    else return c16 >= 8 - G && c16 < 8;
+}
+template <int G>
+__device__ __forceinline__ int col_head(int c16) {  // query head of a hi or lo column
+    if constexpr (G == 8) return c16 & 7;
+    else return c16 < G ? c16 : (col_is_lo<G>(c16) ? 7 - c16 : 0);
+}
+// the value of the partner column's lane (same row, same 4-key group)
+template <int G>
+__device__ __forceinline__ float partner(float x) {
+    if constexpr (G == 8) return dpp<0x128>(x);  // row_ror:8
+    else return dpp<0x141>(x);                   // row_half_mirror
 }
 // max over the 4 rows of the wave (lanes l, l ^ 16, l ^ 32, l ^ 48)
 __device__ __forceinline__ float max_rows(float x) {
@@ -727,7 +738,7 @@ decode_f16_kernel(DecodeArgs<NS> a) {
     const int c16 = lane & 15;
     const int u = lane >> 4;
     const bool colq = c16 < G;
-    const bool col_lo = c16 >= G && c16 < 2 * G;
+    const bool col_lo = col_is_lo<G>(c16);
 
     const int s0 = split * sd.chunk;
     const int s1 = min(sd.lk, s0 + sd.chunk);
@@ -741,7 +752,7 @@ decode_f16_kernel(DecodeArgs<NS> a) {
     // Q rows of this lane's column (dims 32 t + 8 u .. + 8 for t < 4), loaded first
     u32x4 qr[8];
     {
-        const uint8_t* qrow = reinterpret_cast<const uint8_t*>(qseq + (size_t)(h0 + (c16 & (G - 1))) * kDim);
+        const uint8_t* qrow = reinterpret_cast<const uint8_t*>(qseq + (size_t)(h0 + col_head<G>(c16)) * kDim);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             qr[2 * t] = ld16_asm(qrow + 4 * (32 * t + 8 * u));
@@ -779,7 +790,7 @@ decode_f16_kernel(DecodeArgs<NS> a) {
     }
 
     // ---- Q^T B-operand: k-step t holds dims 32 t + 8 u + j; column c < G: head h0 + c, hi half;
-    // G <= c < 2 G: the same head, lo half; other columns zero ------------------------------------
+    // its partner column (col_is_lo): the same head, lo half; other columns zero ------------------
     half8 qb[4];
     {
         const float sc = (colq || col_lo) ? a.scale : 0.0f;
@@ -822,17 +833,23 @@ decode_f16_kernel(DecodeArgs<NS> a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) x[kt][r] = sacc[r];
         }
-        // hi + lo: lanes c and c ^ G add the same two values, so both hold the same bits
+        // hi + lo: a lane and its partner add the same two values, so both hold the same bits
         float bm = -INFINITY;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float v = x[kt][r] + xor_row<G>(x[kt][r], c16);
-                const bool ok = jb + 16 * kt + 4 * u + r < s1;
-                x[kt][r] = ok ? v * kLog2e : -INFINITY;
-                bm = fmaxf(bm, x[kt][r]);
-            }
+            for (int r = 0; r < 4; ++r) x[kt][r] = (x[kt][r] + partner<G>(x[kt][r])) * kLog2e;
+        if (jb + kBlock > s1) {  // the split's last block: keys past its end get -inf
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (jb + 16 * kt + 4 * u + r >= s1) x[kt][r] = -INFINITY;
+        }
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) bm = fmaxf(bm, x[kt][r]);
         bm = max_rows(bm);  // finite: key jb is valid
         // lazy reference point: rescale O only when some column's max grew by more than 2^8
         if (__builtin_amdgcn_ballot_w64(bm > mref + kLazyRescale) != 0) {
@@ -880,7 +897,7 @@ decode_f16_kernel(DecodeArgs<NS> a) {
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[dt][r] += xor_row<G>(acc[dt][r], c16);
+        for (int r = 0; r < 4; ++r) acc[dt][r] += partner<G>(acc[dt][r]);
     // the merge area has its own LDS when it fits beside the ring; otherwise it reuses the V
     // slots once every wave is done with them (all copies waited for)
     float* fin;
@@ -942,7 +959,7 @@ decode_q8_kernel(DecodeArgs<NS> a) {
     const int c16 = lane & 15;
     const int u = lane >> 4;
     const bool colq = c16 < G;
-    const bool col_lo = c16 >= G && c16 < 2 * G;
+    const bool col_lo = col_is_lo<G>(c16);
 
     const int s0 = split * sd.chunk;
     const int s1 = min(sd.lk, s0 + sd.chunk);
@@ -954,7 +971,7 @@ decode_q8_kernel(DecodeArgs<NS> a) {
 
     u32x4 qr[8];
     {
-        const uint8_t* qrow = reinterpret_cast<const uint8_t*>(qseq + (size_t)(h0 + (c16 & (G - 1))) * kDim);
+        const uint8_t* qrow = reinterpret_cast<const uint8_t*>(qseq + (size_t)(h0 + col_head<G>(c16)) * kDim);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             qr[2 * t] = ld16_asm(qrow + 4 * (32 * t + 8 * u));
@@ -1091,12 +1108,18 @@ decode_q8_kernel(DecodeArgs<NS> a) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float v = x[kt][r] + xor_row<G>(x[kt][r], c16);
-                const bool ok = jb + 16 * kt + 4 * u + r < s1;
-                x[kt][r] = ok ? v * kLog2e : -INFINITY;
-                bm = fmaxf(bm, x[kt][r]);
-            }
+            for (int r = 0; r < 4; ++r) x[kt][r] = (x[kt][r] + partner<G>(x[kt][r])) * kLog2e;
+        if (jb + kBlock > s1) {  // the split's last block: keys past its end get -inf
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (jb + 16 * kt + 4 * u + r >= s1) x[kt][r] = -INFINITY;
+        }
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) bm = fmaxf(bm, x[kt][r]);
         bm = max_rows(bm);
         if (__builtin_amdgcn_ballot_w64(bm > mref + kLazyRescaleQ8) != 0) {
             const float mn = fmaxf(mref, bm);
@@ -1202,7 +1225,7 @@ decode_q8_kernel(DecodeArgs<NS> a) {
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[dt][r] += xor_row<G>(acc[dt][r], c16);
+        for (int r = 0; r < 4; ++r) acc[dt][r] += partner<G>(acc[dt][r]);
     __syncthreads();  // every wave is done with its slots (all copies waited for)
     DECODE_STAMP(kStampWaveDone);
     finish_split<G, W, HPW>(a, sd, si, row, split, reinterpret_cast<float*>(&s_slot[0][0][0]),
