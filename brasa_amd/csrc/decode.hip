@@ -823,6 +823,17 @@ decode_f16_kernel(DecodeArgs<NS> a) {
         if (i == 0) DECODE_STAMP(kStampFirstBlock);
         if (i + 1 == nb) DECODE_STAMP(kStampLastBlock);
         const int jb = s0 + kBlock * (ks + KS * i);
+        // the V^T operands, read from LDS now (the block has landed) so the reads return while
+        // S^T and the softmax are computed (after the rescale branch they waited for them)
+        const uint16_t* vt = &s_v[wave][S][0];
+        half8 va[8];
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            const int off = ((((2 * dt + (trc >> 1)) ^ (2 * trj))) << 3) + 4 * (trc & 1);
+            const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vt + (4 * u + trj) * kDim + off));
+            const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vt + (16 + 4 * u + trj) * kDim + off));
+            va[dt] = __builtin_bit_cast(half8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
         // S^T tiles: rows = keys jb + 16 kt + 4 u + r, column = head (hi / lo half)
         float x[2][4];
 #pragma unroll
@@ -869,15 +880,8 @@ decode_f16_kernel(DecodeArgs<NS> a) {
         lsum += ps;
         const half8 pb = split8_sel(p, col_lo);
         // O^T += V^T P^T; P^T slot j of lane (c, u) is key j < 4 ? 4u + j : 16 + 4u + j - 4
-        const uint16_t* vt = &s_v[wave][S][0];
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-            const int off = ((((2 * dt + (trc >> 1)) ^ (2 * trj))) << 3) + 4 * (trc & 1);
-            const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vt + (4 * u + trj) * kDim + off));
-            const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vt + (16 + 4 * u + trj) * kDim + off));
-            const half8 va = __builtin_bit_cast(half8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
-            acc[dt] = mfma16(va, pb, acc[dt]);
-        }
+        for (int dt = 0; dt < 8; ++dt) acc[dt] = mfma16(va[dt], pb, acc[dt]);
         if (i + kRing < nb) {
             // the slot's LDS reads have returned (their values fed the MFMAs above) before the
             // next block's copies into it are issued
@@ -897,7 +901,13 @@ decode_f16_kernel(DecodeArgs<NS> a) {
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[dt][r] += partner<G>(acc[dt][r]);
+        for (int r = 0; r < 4; ++r) {
+            acc[dt][r] += partner<G>(acc[dt][r]);
+            // every lane adds here (one v_add_f32_dpp), before the hi lanes' LDS stores: left
+            // to itself, the compiler moved the adds into their masked region and the exchanges
+            // became separate moves with zeroed destinations
+            asm volatile("" : "+v"(acc[dt][r]));
+        }
     // the merge area has its own LDS when it fits beside the ring; otherwise it reuses the V
     // slots once every wave is done with them (all copies waited for)
     float* fin;
@@ -1225,7 +1235,13 @@ decode_q8_kernel(DecodeArgs<NS> a) {
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[dt][r] += partner<G>(acc[dt][r]);
+        for (int r = 0; r < 4; ++r) {
+            acc[dt][r] += partner<G>(acc[dt][r]);
+            // every lane adds here (one v_add_f32_dpp), before the hi lanes' LDS stores: left
+            // to itself, the compiler moved the adds into their masked region and the exchanges
+            // became separate moves with zeroed destinations
+            asm volatile("" : "+v"(acc[dt][r]));
+        }
     __syncthreads();  // every wave is done with its slots (all copies waited for)
     DECODE_STAMP(kStampWaveDone);
     finish_split<G, W, HPW>(a, sd, si, row, split, reinterpret_cast<float*>(&s_slot[0][0][0]),
