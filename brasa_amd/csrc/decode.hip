@@ -268,6 +268,20 @@ __device__ __forceinline__ int q8_exp(uint16_t sc) {
 // 16-byte reads (lane 2 r + h reads chunk 4 h + j of row r) then hit distinct bank groups.
 __device__ __forceinline__ int q8_vswz(int r) { return (r ^ (r >> 2)) & 3; }
 
+// max over the 4 rows of the wave (lanes l, l ^ 16, l ^ 32, l ^ 48)
+__device__ __forceinline__ float max_rows(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
+    x = fmaxf(__int_as_float(a[0]), __int_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+    return fmaxf(__int_as_float(b[0]), __int_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_rows(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
+    x = __int_as_float(a[0]) + __int_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+    return __int_as_float(b[0]) + __int_as_float(b[1]);
+}
+
 // ---- the end of a split: merge the W waves, then the splits --------------------------------
 // (M, A, L) <- merge of (M, A, L) and (m, a, l): M = max, weights 2^(m - M) (0 for an empty side)
 __device__ __forceinline__ void merge_split(float& M, f32x4& A, float& L, float m, f32x4 a,
@@ -384,7 +398,13 @@ __device__ __forceinline__ void finish_split(const DecodeArgs<NS>& a, const SeqD
 
     constexpr int NSG = 64 * W / (HG * 32);  // split groups
     static_assert(NSG >= 1 && NSG * HG * 32 == 64 * W, "final-merge thread layout");
-    const int q = threadIdx.x & 31, cc = (threadIdx.x >> 5) % HG, sg = threadIdx.x / (32 * HG);
+    // With 4 split groups they sit in lane bits 4 and 5 (lanes l, l ^ 16, l ^ 32, l ^ 48 of a
+    // wave hold one (query head, dims) item), so the groups are folded by permlane swaps inside
+    // the wave, with no LDS round trip or barrier; otherwise in LDS after the loop.
+    constexpr bool kLaneGroups = NSG == 4;
+    const int item = kLaneGroups ? ((threadIdx.x & 15) | ((threadIdx.x >> 6) << 4)) : threadIdx.x;
+    const int q = item & 31, cc = (item >> 5) % HG;
+    const int sg = kLaneGroups ? (threadIdx.x >> 4) & 3 : threadIdx.x / (32 * HG);
     const int h = min(q0 + cc, a.hq - 1);  // (duplicate work past hq is not stored)
     const float* pa = part_acc + (size_t)h * splits * kDim + 4 * q;
     const float* pm = part_ml + (size_t)h * splits * 2;
@@ -420,7 +440,15 @@ __device__ __forceinline__ void finish_split(const DecodeArgs<NS>& a, const SeqD
         }
         merge_split(M, A, L, Mr, Ar, Lr);
     }
-    if constexpr (NSG > 1) {
+    if constexpr (kLaneGroups) {
+        // max first, then the weighted sums: every lane of the four adds the same values in
+        // the same pairs (l with l ^ 16, then with l ^ 32), so all four hold the same bits
+        const float Mx = max_rows(M);
+        const float w = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - Mx);
+        A = f32x4{sum_rows(A.x * w), sum_rows(A.y * w), sum_rows(A.z * w), sum_rows(A.w * w)};
+        L = sum_rows(L * w);
+        if (sg != 0) return;
+    } else if constexpr (NSG > 1) {
         f32x4* r_a = reinterpret_cast<f32x4*>(lds);  // [NSG][HG][32], then m and l
         float* r_m = lds + 4 * 64 * W;
         float* r_l = r_m + 64 * W;
@@ -693,19 +721,6 @@ template <int G>
 __device__ __forceinline__ float partner(float x) {
     if constexpr (G == 8) return dpp<0x128>(x);  // row_ror:8
     else return dpp<0x141>(x);                   // row_half_mirror
-}
-// max over the 4 rows of the wave (lanes l, l ^ 16, l ^ 32, l ^ 48)
-__device__ __forceinline__ float max_rows(float x) {
-    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
-    x = fmaxf(__int_as_float(a[0]), __int_as_float(a[1]));
-    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
-    return fmaxf(__int_as_float(b[0]), __int_as_float(b[1]));
-}
-__device__ __forceinline__ float sum_rows(float x) {
-    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_int(x), __float_as_int(x), false, false);
-    x = __int_as_float(a[0]) + __int_as_float(a[1]);
-    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
-    return __int_as_float(b[0]) + __int_as_float(b[1]);
 }
 
 template <int G, int NS, int HPW, int W>
