@@ -356,7 +356,44 @@ __device__ __forceinline__ void finish_split(const DecodeArgs<NS>& a, const SeqD
     const int q0 = row * HG;
     float* part_acc = a.part + sd.part_off;
     float* part_ml = part_acc + (size_t)a.hq * splits * kDim;
-    for (int idx = threadIdx.x; idx < HG * 32; idx += 64 * W) {
+    // With 4 x 32 x HG = 64 W threads and KS a multiple of 4, every thread takes a quarter of
+    // the waves of one (query head, dims) item, and the quarters (lanes l, l ^ 16, l ^ 32,
+    // l ^ 48) are folded by permlane swaps; the lanes with quarter 0 store.
+    constexpr bool kLaneQuarters = HG * 32 * 4 == 64 * W && KS % 4 == 0;
+    if constexpr (kLaneQuarters) {
+        constexpr int KQ = KS / 4;
+        const int item = (threadIdx.x & 15) | ((threadIdx.x >> 6) << 4);
+        const int kq = (threadIdx.x >> 4) & 3;
+        const int hm = item / (G * 32), c = (item >> 5) % G, d = 4 * (item & 31);
+        const int h = q0 + hm * G + c;
+        float Mq = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < KQ; ++k) Mq = fmaxf(Mq, m_ml[(((kq * KQ + k) * HPW + hm) * G + c) * 2]);
+        f32x4 A = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        float L = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KQ; ++k) {
+            const int wv = ((kq * KQ + k) * HPW + hm) * G + c;
+            const float mw = m_ml[wv * 2];
+            const float e = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - Mq);
+            A += e * *reinterpret_cast<const f32x4*>(m_acc + wv * kDim + d);
+            L += e * m_ml[wv * 2 + 1];
+        }
+        // the quarters: max first, then the weighted sums (the same bits in all four lanes)
+        const float M = max_rows(Mq);
+        const float w = Mq == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(Mq - M);
+        A = f32x4{sum_rows(A.x * w), sum_rows(A.y * w), sum_rows(A.z * w), sum_rows(A.w * w)};
+        L = sum_rows(L * w);
+        if (kq == 0 && h < a.hq) {
+            if (splits == 1) {
+                store_out(a, si, h, d, A / L);
+            } else {
+                st_dev16(part_acc + ((size_t)h * splits + split) * kDim + d, A);
+                if (d == 0) st_dev8(part_ml + ((size_t)h * splits + split) * 2, f32x2{M, L});
+            }
+        }
+    }
+    for (int idx = threadIdx.x; !kLaneQuarters && idx < HG * 32; idx += 64 * W) {
         const int hm = idx / (G * 32), c = (idx >> 5) % G, d = 4 * (idx & 31);
         const int h = q0 + hm * G + c;
         if (h >= a.hq) continue;  // a partial last row of head groups
