@@ -451,16 +451,39 @@ __device__ __forceinline__ void finish_split(const DecodeArgs<NS>& a, const SeqD
     for (int s0 = sg; s0 < splits; s0 += kPer * NSG) {
         f32x4 av[kPer];
         f32x2 mv[kPer];
+        if constexpr (kLaneGroups) {
+            // The 16 lanes of a split group (one query head) need the same kPer (m, l) pairs:
+            // lane j of the group loads pair j % kPer, and the pairs go to the others through
+            // the wave's own LDS slots (one load instead of kPer with 16 equal addresses each;
+            // the loads' address processing is the merge's bottleneck)
+            f32x2 mine;
 #pragma unroll
-        for (int r = 0; r < kPer; ++r) {
-            const int sp = min(s0 + NSG * r, splits - 1);
-            av[r] = ld_dev16(pa + (size_t)sp * kDim);
-            mv[r] = ld_dev8(pm + (size_t)sp * 2);
+            for (int r = 0; r < kPer; ++r)
+                av[r] = ld_dev16(pa + (size_t)min(s0 + NSG * r, splits - 1) * kDim);
+            mine = ld_dev8(pm + (size_t)min(s0 + NSG * ((threadIdx.x & 15) % kPer), splits - 1) * 2);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            DECODE_STAMP(kStampLoaded);
+#pragma unroll
+            for (int r = 0; r < kPer; ++r) asm volatile("" : "+v"(av[r]));
+            asm volatile("" : "+v"(mine));
+            // lds: 64 W (m, l) slots, free here (the wave merge's reads are done)
+            f32x2* slots = reinterpret_cast<f32x2*>(lds);
+            slots[threadIdx.x] = mine;
+            const f32x2* grp = slots + (threadIdx.x & ~15);  // this wave's group of 16 lanes
+#pragma unroll
+            for (int r = 0; r < kPer; ++r) mv[r] = grp[r];
+        } else {
+#pragma unroll
+            for (int r = 0; r < kPer; ++r) {
+                const int sp = min(s0 + NSG * r, splits - 1);
+                av[r] = ld_dev16(pa + (size_t)sp * kDim);
+                mv[r] = ld_dev8(pm + (size_t)sp * 2);
+            }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            DECODE_STAMP(kStampLoaded);
+#pragma unroll
+            for (int r = 0; r < kPer; ++r) asm volatile("" : "+v"(av[r]), "+v"(mv[r]));
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        DECODE_STAMP(kStampLoaded);
-#pragma unroll
-        for (int r = 0; r < kPer; ++r) asm volatile("" : "+v"(av[r]), "+v"(mv[r]));
         // this round's splits: max first, then the weighted sums in split order
         float Mr = -INFINITY;
 #pragma unroll
