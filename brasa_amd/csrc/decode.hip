@@ -307,10 +307,11 @@ __device__ __forceinline__ void store_out(const DecodeArgs<NS>& a, int si, int h
     }
 }
 
-// LDS floats finish_split needs: the W waves' states, then the final merge's split groups.
+// LDS floats finish_split needs: the W waves' states, then the final merge's split groups and
+// its (m, l) slots.
 template <int G, int W>
 constexpr int finish_floats() {
-    return W * G * (kDim + 2) > 64 * W * 6 ? W * G * (kDim + 2) : 64 * W * 6;
+    return W * G * (kDim + 2) > 64 * W * 8 ? W * G * (kDim + 2) : 64 * W * 8;
 }
 
 // Every thread of the workgroup calls this once its wave's blocks are done. The workgroup serves
@@ -451,38 +452,30 @@ __device__ __forceinline__ void finish_split(const DecodeArgs<NS>& a, const SeqD
     for (int s0 = sg; s0 < splits; s0 += kPer * NSG) {
         f32x4 av[kPer];
         f32x2 mv[kPer];
-        if constexpr (kLaneGroups) {
-            // The 16 lanes of a split group (one query head) need the same kPer (m, l) pairs:
-            // lane j of the group loads pair j % kPer, and the pairs go to the others through
-            // the wave's own LDS slots (one load instead of kPer with 16 equal addresses each;
-            // the loads' address processing is the merge's bottleneck)
+        {
+            // The GL lanes of a split group (one query head and split group: 16 lanes with the
+            // groups in lane bits 4-5, else 32) need the same kPer (m, l) pairs: lane j of the
+            // group loads pair j % kPer, and the pairs go to the others through the wave's own
+            // LDS slots (one load instead of kPer with GL equal addresses each; the loads'
+            // address processing is the merge's bottleneck)
+            constexpr int GL = kLaneGroups ? 16 : 32;
             f32x2 mine;
 #pragma unroll
             for (int r = 0; r < kPer; ++r)
                 av[r] = ld_dev16(pa + (size_t)min(s0 + NSG * r, splits - 1) * kDim);
-            mine = ld_dev8(pm + (size_t)min(s0 + NSG * ((threadIdx.x & 15) % kPer), splits - 1) * 2);
+            mine = ld_dev8(pm + (size_t)min(s0 + NSG * ((threadIdx.x & (GL - 1)) % kPer), splits - 1) * 2);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             DECODE_STAMP(kStampLoaded);
 #pragma unroll
             for (int r = 0; r < kPer; ++r) asm volatile("" : "+v"(av[r]));
             asm volatile("" : "+v"(mine));
-            // lds: 64 W (m, l) slots, free here (the wave merge's reads are done)
-            f32x2* slots = reinterpret_cast<f32x2*>(lds);
+            // 64 W (m, l) slots past the split-group fold's area (the wave merge's reads of
+            // this LDS are done; a wave can reach the fold while another still reads its slots)
+            f32x2* slots = reinterpret_cast<f32x2*>(lds + 6 * 64 * W);
             slots[threadIdx.x] = mine;
-            const f32x2* grp = slots + (threadIdx.x & ~15);  // this wave's group of 16 lanes
+            const f32x2* grp = slots + (threadIdx.x & ~(GL - 1));  // this lane's group
 #pragma unroll
             for (int r = 0; r < kPer; ++r) mv[r] = grp[r];
-        } else {
-#pragma unroll
-            for (int r = 0; r < kPer; ++r) {
-                const int sp = min(s0 + NSG * r, splits - 1);
-                av[r] = ld_dev16(pa + (size_t)sp * kDim);
-                mv[r] = ld_dev8(pm + (size_t)sp * 2);
-            }
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            DECODE_STAMP(kStampLoaded);
-#pragma unroll
-            for (int r = 0; r < kPer; ++r) asm volatile("" : "+v"(av[r]), "+v"(mv[r]));
         }
         // this round's splits: max first, then the weighted sums in split order
         float Mr = -INFINITY;
