@@ -86,10 +86,12 @@ __global__ void rope_neox_kernel(float* x, const float* __restrict__ cos_t,
     v[i + half] = b * c + a * s;
 }
 
-// Writes this lane's two elements (l and l + 64) of cache row `row`.
+// Writes this lane's two elements (l and l + 64) of cache row `row`. q8_0 rows go through
+// `stage` (this wave's 136-byte LDS row): the codes and scales are written there byte by byte and
+// the row leaves as 34 dword stores (one instruction) instead of two byte stores per lane.
 template <int KV>
 __device__ __forceinline__ void store_row(uint8_t* cache, size_t row, int lane, float y0,
-                                          float y1) {
+                                          float y1, uint8_t* stage) {
     if constexpr (KV == BRASA_KV_F32) {
         float* r = reinterpret_cast<float*>(cache) + row * kDim;
         r[lane] = y0;
@@ -100,16 +102,19 @@ __device__ __forceinline__ void store_row(uint8_t* cache, size_t row, int lane, 
         r[lane + 64] = f2h(y1);
     } else {
         // groups: elements 32 g .. 32 g + 31; y0 is in group lane / 32, y1 in 2 + lane / 32
-        uint8_t* r = cache + row * kQ8Row;
         const uint16_t d0 = q8_scale_bits(half_wave_max(fabsf(y0)));
         const uint16_t d1 = q8_scale_bits(half_wave_max(fabsf(y1)));
-        r[lane] = (uint8_t)q8_code(y0, h2f(d0));
-        r[lane + 64] = (uint8_t)q8_code(y1, h2f(d1));
+        stage[lane] = (uint8_t)q8_code(y0, h2f(d0));
+        stage[lane + 64] = (uint8_t)q8_code(y1, h2f(d1));
         if ((lane & 31) == 0) {
-            uint16_t* sc = reinterpret_cast<uint16_t*>(r + 128);
+            uint16_t* sc = reinterpret_cast<uint16_t*>(stage + 128);
             sc[lane >> 5] = d0;
             sc[2 + (lane >> 5)] = d1;
         }
+        // (one wave: its LDS writes are done before its reads; the next row's writes come after)
+        if (lane < kQ8Row / 4)
+            reinterpret_cast<uint32_t*>(cache + row * kQ8Row)[lane] =
+                reinterpret_cast<const uint32_t*>(stage)[lane];
     }
 }
 
@@ -132,8 +137,10 @@ struct QkvArgs {
 // 4 w .. 4 w + 3.
 template <int KV>
 __global__ void __launch_bounds__(64 * kWavesPerWg) qk_norm_rope_store_kernel(QkvArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_stage[kWavesPerWg][KV == BRASA_KV_Q8_0 ? kQ8Row : 4];
     const int gr0 = (blockIdx.x * kWavesPerWg + (threadIdx.x >> 6)) * kRowsPerWave;
     const int lane = threadIdx.x & 63;
+    uint8_t* stage = s_stage[threadIdx.x >> 6];
     if (gr0 >= a.rows) return;
     const int per_tok = a.hq + 2 * a.hkv;
     float x0[kRowsPerWave], x1[kRowsPerWave], w0[kRowsPerWave], w1[kRowsPerWave];
@@ -173,7 +180,7 @@ __global__ void __launch_bounds__(64 * kWavesPerWg) qk_norm_rope_store_kernel(Qk
     for (int j = 0; j < kRowsPerWave; ++j) {
         if (kind[j] == 3) break;
         if (kind[j] == 2) {
-            store_row<KV>(a.vc, crow[j], lane, x0[j], x1[j]);
+            store_row<KV>(a.vc, crow[j], lane, x0[j], x1[j], stage);
             continue;
         }
         float p = 0.0f;
@@ -186,7 +193,7 @@ __global__ void __launch_bounds__(64 * kWavesPerWg) qk_norm_rope_store_kernel(Qk
         const float y1 = b0 * c[j] + a0 * sn[j];
         dst[j][lane] = y0;
         dst[j][lane + 64] = y1;
-        if (kind[j] == 1) store_row<KV>(a.kc, crow[j], lane, y0, y1);
+        if (kind[j] == 1) store_row<KV>(a.kc, crow[j], lane, y0, y1, stage);
     }
 }
 
