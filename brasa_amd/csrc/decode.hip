@@ -321,7 +321,8 @@ constexpr int finish_floats() {
 // summed over the hi / lo columns; mref the column's reference point (log2 domain, -inf for a
 // wave without keys) and lsum its softmax denominator (summed over the wave's rows). `lds` holds
 // finish_floats<G, W>() floats that no wave still reads.
-//  1. The W / HPW waves of each head group merge through LDS in wave order. A sequence with one
+//  1. The W / HPW waves of each head group merge through LDS (in wave order, or by quarters of
+//     the waves folded with permlane swaps when the thread layout allows). A sequence with one
 //     split writes o here.
 //  2. Otherwise the workgroup stores its partials (acc [hq][splits][128], then (m, l)
 //     [hq][splits][2], the reference's scratch layout), waits until the stores are
@@ -330,9 +331,10 @@ constexpr int finish_floats() {
 //  3. The last arrival merges every split: thread (sg, cc, q) takes splits sg, sg + NSG, ... of
 //     query head q0 + cc, dims 4 q .. 4 q + 3, kPer per round trip; each round is folded as max
 //     first, then sum_r 2^(m_r - max) (acc_r, l_r) in split order (a short dependency chain),
-//     rounds and then the NSG split groups (through LDS) are folded the same way, and
-//     o = A / L is written. The order is fixed, so the result does not depend on which
-//     workgroup is last.
+//     rounds and then the NSG split groups (by permlane swaps when they sit in lane bits 4-5,
+//     else through LDS) are folded the same way, and o = A / L is written. The (m, l) pairs of a
+//     round are loaded once per group of lanes that share them and passed on through LDS. The
+//     order is fixed, so the result does not depend on which workgroup is last.
 template <int G, int W, int HPW, int NS>
 __device__ __forceinline__ void finish_split(const DecodeArgs<NS>& a, const SeqDesc& sd, int si,
                                              int row, int split, float* lds,
