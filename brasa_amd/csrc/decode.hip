@@ -1157,26 +1157,109 @@ decode_q8_kernel(DecodeArgs<NS> a) {
         uint8_t* sl = &s_slot[wave][S][0];
         const uint8_t* ksc = sl + 2 * kQ8Codes;
         const uint8_t* vsc = sl + 2 * kQ8Codes + 256;
+        // K codes (the MFMA A layout) and the rows' K scales into registers first: the V tile
+        // below is written over the block's code area
+        u32x2 kc[2][4], ksw[2][4];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            const int r = 16 * kt + c16;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int L = 2 * t + (u >> 1);
+                kc[kt][t] = *reinterpret_cast<const u32x2*>(sl + r * 128 + 16 * (L ^ ((r >> 1) & 7)) + 8 * (u & 1));
+            }
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)  // scales of S row 16 kt + 4 u + rr
+                ksw[kt][rr] = *reinterpret_cast<const u32x2*>(ksc + (16 * kt + 4 * u + rr) * 8);
+        }
+        // V codes -> f16 * 2^e tile over the block's code area (the f16 kernel's tr16 layout);
+        // the same lane also writes the mantissa factors scale * 2^-e of its row's two groups
+        // to the slot's factor table, read back below to fold them into P. Done before S^T: the
+        // V^T operand and factor reads then return while S^T and the softmax are computed.
+        float* fac = reinterpret_cast<float*>(sl + kQ8Fac);  // [key][group]
+        {
+            u32x4 vc[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                vc[j] = *reinterpret_cast<const u32x4*>(sl + kQ8Codes + vr * 128 +
+                                                        16 * ((4 * vh + j) ^ q8_vswz(vr)));
+            const uint32_t vs = *reinterpret_cast<const uint32_t*>(vsc + vr * 8 + 4 * vh);
+            const uint16_t sc2[2] = {(uint16_t)(vs & 0xffffu), (uint16_t)(vs >> 16)};
+            int ex[2];
+            float fm[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                ex[q] = q8_exp(sc2[q]);
+                fm[q] = __builtin_amdgcn_ldexpf(h2f(sc2[q]), -ex[q]);
+            }
+            // every LDS read of the code area (K codes and scales above included) has returned
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) asm volatile("" : "+v"(kc[kt][t]), "+v"(ksw[kt][t]));
+            asm volatile("" ::: "memory");
+            *reinterpret_cast<f32x2*>(fac + vr * 4 + 2 * vh) = f32x2{fm[0], fm[1]};
+            uint16_t* vt = reinterpret_cast<uint16_t*>(sl);
+            // per group: the conversion magic's exponent byte and bias for 2^e (codes4_to_f16_exp)
+            uint32_t eb[2], bias[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                eb[q] = (uint32_t)(4 * (ex[q] + 25)) * 0x01010101u;
+                const uint32_t b16 = (uint32_t)__builtin_bit_cast(
+                    uint16_t, (_Float16)__builtin_amdgcn_ldexpf(-1152.0f, ex[q]));
+                bias[q] = b16 | (b16 << 16);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t w[4] = {vc[j].x, vc[j].y, vc[j].z, vc[j].w};
+                uint32_t hv[8];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    codes4_to_f16_exp(w[e], eb[j >> 1], bias[j >> 1], hv[2 * e], hv[2 * e + 1]);
+                // 16 codes = dims 64 vh + 16 j .. + 16: logical chunks 8 vh + 2 j, + 1 of row vr
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const int lc2 = 8 * vh + 2 * j + q;
+                    *reinterpret_cast<u32x4*>(vt + vr * kDim + 8 * (lc2 ^ (2 * (vr & 3)))) =
+                        u32x4{hv[4 * q], hv[4 * q + 1], hv[4 * q + 2], hv[4 * q + 3]};
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // tile and factors written before they are read
+            asm volatile("" ::: "memory");
+        }
+        // the V^T operands and the factors of this lane's keys, read now, used after the softmax
+        const uint16_t* vtr = reinterpret_cast<const uint16_t*>(sl);
+        half8 va[8];
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            const int off = ((((2 * dt + (trc >> 1)) ^ (2 * trj))) << 3) + 4 * (trc & 1);
+            const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vtr + (4 * u + trj) * kDim + off));
+            const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vtr + (16 + 4 * u + trj) * kDim + off));
+            va[dt] = __builtin_bit_cast(half8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+        f32x4 fk[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int key = (j < 4) ? 4 * u + j : 16 + 4 * u + (j - 4);
+            fk[j] = *reinterpret_cast<const f32x4*>(fac + key * 4);
+        }
         // S^T: per 32-dim group t one MFMA (codes as f16), scaled by the row's group scale
         float x[2][4];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
-            const int r = 16 * kt + c16;
             f32x4 part[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const int L = 2 * t + (u >> 1);
-                const u32x2 c = *reinterpret_cast<const u32x2*>(sl + r * 128 + 16 * (L ^ ((r >> 1) & 7)) + 8 * (u & 1));
                 uint32_t h0l, h0h, h1l, h1h;
-                codes4_to_f16(c.x, h0l, h0h);
-                codes4_to_f16(c.y, h1l, h1h);
+                codes4_to_f16(kc[kt][t].x, h0l, h0h);
+                codes4_to_f16(kc[kt][t].y, h1l, h1h);
                 const u32x4 h = u32x4{h0l, h0h, h1l, h1h};
                 part[t] = mfma16(as_half8(h), qb[t], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
             }
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
-                // scales of S row 16 kt + 4 u + rr
-                const u32x2 sw = *reinterpret_cast<const u32x2*>(ksc + (16 * kt + 4 * u + rr) * 8);
+                const u32x2 sw = ksw[kt][rr];
                 float v = part[0][rr] * h2f((uint16_t)(sw.x & 0xffffu));
                 v = fmaf(part[1][rr], h2f((uint16_t)(sw.x >> 16)), v);
                 v = fmaf(part[2][rr], h2f((uint16_t)(sw.y & 0xffffu)), v);
@@ -1216,82 +1299,17 @@ decode_q8_kernel(DecodeArgs<NS> a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) ps += p[j];
         lsum += ps;
-        // V codes -> f16 * 2^e tile over the block's code area (the f16 kernel's tr16 layout);
-        // the same lane also writes the mantissa factors scale * 2^-e of its row's two groups
-        // to the slot's factor table, read back below to fold them into P
-        float* fac = reinterpret_cast<float*>(sl + kQ8Fac);  // [key][group]
-        {
-            u32x4 vc[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                vc[j] = *reinterpret_cast<const u32x4*>(sl + kQ8Codes + vr * 128 +
-                                                        16 * ((4 * vh + j) ^ q8_vswz(vr)));
-            const uint32_t vs = *reinterpret_cast<const uint32_t*>(vsc + vr * 8 + 4 * vh);
-            const uint16_t sc2[2] = {(uint16_t)(vs & 0xffffu), (uint16_t)(vs >> 16)};
-            int ex[2];
-            float fm[2];
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                ex[q] = q8_exp(sc2[q]);
-                fm[q] = __builtin_amdgcn_ldexpf(h2f(sc2[q]), -ex[q]);
-            }
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // every LDS read of the code area has returned
-            asm volatile("" ::: "memory");
-            *reinterpret_cast<f32x2*>(fac + vr * 4 + 2 * vh) = f32x2{fm[0], fm[1]};
-            uint16_t* vt = reinterpret_cast<uint16_t*>(sl);
-            // per group: the conversion magic's exponent byte and bias for 2^e (codes4_to_f16_exp)
-            uint32_t eb[2], bias[2];
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                eb[q] = (uint32_t)(4 * (ex[q] + 25)) * 0x01010101u;
-                const uint32_t b16 = (uint32_t)__builtin_bit_cast(
-                    uint16_t, (_Float16)__builtin_amdgcn_ldexpf(-1152.0f, ex[q]));
-                bias[q] = b16 | (b16 << 16);
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t w[4] = {vc[j].x, vc[j].y, vc[j].z, vc[j].w};
-                uint32_t hv[8];
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    codes4_to_f16_exp(w[e], eb[j >> 1], bias[j >> 1], hv[2 * e], hv[2 * e + 1]);
-                // 16 codes = dims 64 vh + 16 j .. + 16: logical chunks 8 vh + 2 j, + 1 of row vr
-#pragma unroll
-                for (int q = 0; q < 2; ++q) {
-                    const int lc2 = 8 * vh + 2 * j + q;
-                    *reinterpret_cast<u32x4*>(vt + vr * kDim + 8 * (lc2 ^ (2 * (vr & 3)))) =
-                        u32x4{hv[4 * q], hv[4 * q + 1], hv[4 * q + 2], hv[4 * q + 3]};
-                }
-            }
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // tile and factors written before they are read
-            asm volatile("" ::: "memory");
-        }
         // P^T per 32-dim group g: p times the mantissa factor of the key's V scale, hi / lo split
         half8 pb[4];
-        {
-            f32x4 fk[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int key = (j < 4) ? 4 * u + j : 16 + 4 * u + (j - 4);
-                fk[j] = *reinterpret_cast<const f32x4*>(fac + key * 4);
-            }
+        for (int g = 0; g < 4; ++g) {
+            float fg[8];
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                float fg[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) fg[j] = fk[j][g];
-                pb[g] = split8_prod_sel(p, fg, col_lo);
-            }
+            for (int j = 0; j < 8; ++j) fg[j] = fk[j][g];
+            pb[g] = split8_prod_sel(p, fg, col_lo);
         }
-        const uint16_t* vt = reinterpret_cast<const uint16_t*>(sl);
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-            const int off = ((((2 * dt + (trc >> 1)) ^ (2 * trj))) << 3) + 4 * (trc & 1);
-            const v4s lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vt + (4 * u + trj) * kDim + off));
-            const v4s hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(vt + (16 + 4 * u + trj) * kDim + off));
-            const half8 va = __builtin_bit_cast(half8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
-            acc[dt] = mfma16(va, pb[dt >> 1], acc[dt]);
-        }
+        for (int dt = 0; dt < 8; ++dt) acc[dt] = mfma16(va[dt], pb[dt >> 1], acc[dt]);
     };
     for (int i0 = 0; i0 < nb; i0 += kRing) {
         step(I0{}, i0);
