@@ -742,11 +742,6 @@ __device__ __forceinline__ u32x4 ld16_asm(const uint8_t* p) {
     asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
     return r;
 }
-__device__ __forceinline__ u32x4 ld16_nt_asm(const uint8_t* p) {
-    u32x4 r;
-    asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(r) : "v"(p) : "memory");
-    return r;
-}
 // s_waitcnt vmcnt(N) that also "redefines" the 8 K registers of a ring slot, so the compiler
 // cannot move a read of them above the wait.
 template <int N>
@@ -840,7 +835,7 @@ decode_f16_kernel(DecodeArgs<NS> a) {
         for (int kt = 0; kt < 2; ++kt) {
             const uint8_t* row = kbase + (size_t)min(jb + 16 * kt + c16, s1 - 1) * kstride + 16 * u;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) kr[S][4 * kt + t] = ld16_nt_asm(row + 64 * t);
+            for (int t = 0; t < 4; ++t) kr[S][4 * kt + t] = ld16_asm(row + 64 * t);
         }
         uint16_t* vt = &s_v[wave][S][0];
 #pragma unroll
@@ -1011,7 +1006,12 @@ constexpr int kQ8Codes = kBlock * 128;        // bytes of one tile's codes
 constexpr int kQ8Fac = 2 * kQ8Codes + 2 * kBlock * 8;   // K codes, V codes, K scales, V scales,
 constexpr int kQ8Slot = kQ8Fac + kBlock * 4 * 4;         // then V mantissa factors [key][group]
 
-// 4-byte HBM -> LDS copy per lane (global_load_lds_dword, nontemporal): lane i writes lds + 4 i.
+// The copies carry no nontemporal hint (the fp16 kernel's V copies do): a 136-byte row of one KV head
+// shares 128-byte lines with its scale copy and with the adjacent heads (read by the other
+// workgroups of the split on the same XCD, xcd_grid_pos), and cached normally those lines are
+// fetched fewer times (measured: 16K keys 16.2 -> 15.2 us per layer, 32K 25.6 -> 23.2, 4K
+// 9.7 -> 9.5; for the fp16 kernel's V copies the hint is the faster choice, for its K loads
+// plain loads: 17.47 -> 17.33 us at 16K).
 template <int G, int NS, int HPW, int W>
 __global__ void __launch_bounds__(64 * W)
 decode_q8_kernel(DecodeArgs<NS> a) {
@@ -1081,28 +1081,28 @@ decode_q8_kernel(DecodeArgs<NS> a) {
         const uint8_t* vb = sgpr_offset(vbase, (size_t)jb * kstride);
         if (jb + kBlock <= s1) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) lds_dma16_s_nt(kb, off_k[r], sl + 1024 * r);
+            for (int r = 0; r < 4; ++r) lds_dma16_s(kb, off_k[r], sl + 1024 * r);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) lds_dma16_s_nt(vb, off_v[r], sl + kQ8Codes + 1024 * r);
-            lds_dma4_s_nt(kb, off_s, sl + 2 * kQ8Codes);
-            lds_dma4_s_nt(vb, off_s, sl + 2 * kQ8Codes + 256);
+            for (int r = 0; r < 4; ++r) lds_dma16_s(vb, off_v[r], sl + kQ8Codes + 1024 * r);
+            lds_dma4_s(kb, off_s, sl + 2 * kQ8Codes);
+            lds_dma4_s(vb, off_s, sl + 2 * kQ8Codes + 256);
         } else {
             const int last = s1 - 1 - jb;  // rows past it read the last row again
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int rr = 8 * r + lr;
                 const uint32_t row = (uint32_t)(min(rr, last) * kstride);
-                lds_dma16_s_nt(kb, row + 16 * (lc ^ ((rr >> 1) & 7)), sl + 1024 * r);
+                lds_dma16_s(kb, row + 16 * (lc ^ ((rr >> 1) & 7)), sl + 1024 * r);
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int rr = 8 * r + lr;
                 const uint32_t row = (uint32_t)(min(rr, last) * kstride);
-                lds_dma16_s_nt(vb, row + 16 * (lc ^ q8_vswz(rr)), sl + kQ8Codes + 1024 * r);
+                lds_dma16_s(vb, row + 16 * (lc ^ q8_vswz(rr)), sl + kQ8Codes + 1024 * r);
             }
             const uint32_t srow = (uint32_t)(min(sr, last) * kstride) + 128 + 4 * (lane & 1);
-            lds_dma4_s_nt(kb, srow, sl + 2 * kQ8Codes);
-            lds_dma4_s_nt(vb, srow, sl + 2 * kQ8Codes + 256);
+            lds_dma4_s(kb, srow, sl + 2 * kQ8Codes);
+            lds_dma4_s(vb, srow, sl + 2 * kQ8Codes + 256);
         }
     };
     auto issue = [&](auto slot_c, int i) { issue_at(slot_c, s0 + kBlock * (ks + KS * i)); };
