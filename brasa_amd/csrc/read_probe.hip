@@ -8,7 +8,11 @@
 //     32-key blocks of K (16-byte loads into registers) and V (16-byte copies into LDS), the
 //     decode kernel's instructions, for 1, 2 or 4 adjacent KV heads per workgroup;
 //   * contiguous: the same instructions over whole 2 KB key rows (64 keys x 8 heads per workgroup);
-//   * stream: a grid-stride read of both caches, 16 bytes per lane, the plain streaming ceiling.
+//   * stream: a grid-stride read of both caches, 16 bytes per lane, the plain streaming ceiling;
+//   * q8_0 (136-byte rows, 35.7 MB per layer at 16384 keys): 256 workgroups of 8 waves, each
+//     reading the row slices of 1, 2, 4 or 8 adjacent KV heads (HPW x 136 contiguous bytes per
+//     position) of its key range, 8 bytes per lane, every load of a wave issued before it waits;
+//     with and without the nontemporal hint.
 // Build: make -C brasa_amd/csrc read_probe; run: _build/read_probe (one GPU).
 #include <hip/hip_runtime.h>
 
@@ -84,6 +88,37 @@ __global__ void __launch_bounds__(256) stream_kernel(const uint8_t* K, const uin
     if (acc == 0x9e3779b9u) out[0] = acc;  // keeps the loads
 }
 
+// ---- q8_0 ------------------------------------------------------------------------------------
+constexpr size_t kQ8Cache = (size_t)kKeys * kHeads * kQ8Row;
+
+template <int HPW, bool NT>
+__global__ void __launch_bounds__(512) q8_pattern_kernel(const uint8_t* K, const uint8_t* V, unsigned* out) {
+    constexpr int rows = 8 / HPW, splits = 256 / rows, keys = kKeys / splits;
+    constexpr int seg = HPW * kQ8Row;           // bytes per position
+    constexpr int per_wave = keys * seg / 8;    // bytes per wave and cache
+    constexpr int n = per_wave / 512;           // 8-byte loads per lane and cache
+    static_assert(per_wave % 512 == 0, "whole wave loads");
+    const int b = blockIdx.x, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int row = b % rows, key0 = (b / rows) * keys;
+    u32x2 xk[n], xv[n];
+#pragma unroll
+    for (int i = 0; i < n; ++i) {
+        const int byte = w * per_wave + i * 512 + lane * 8;
+        const size_t a = ((size_t)(key0 + byte / seg) * kHeads + row * HPW) * kQ8Row + byte % seg;
+        if constexpr (NT) {
+            xk[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(K + a));
+            xv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(V + a));
+        } else {
+            xk[i] = *reinterpret_cast<const u32x2*>(K + a);
+            xv[i] = *reinterpret_cast<const u32x2*>(V + a);
+        }
+    }
+    u32x2 acc = {0, 0};
+#pragma unroll
+    for (int i = 0; i < n; ++i) acc ^= xk[i] ^ xv[i];
+    if (acc.x == 0x9e3779b9u) out[b] = acc.y;  // keeps the loads
+}
+
 template <class F>
 float time_layers(F launch) {
     hipEvent_t e0, e1;
@@ -139,6 +174,22 @@ int main() {
             snprintf(name, sizeof name, "stream, %d workgroups of 256", nwg);
             line(name, time_layers([&](int l) { stream_kernel<<<nwg, 256>>>(ks[l], vs[l], out, nwg); }));
         }
+    }
+    // q8_0 caches (the f16 buffers are larger than a q8_0 layer: reused)
+    const double mb8 = 2.0 * kQ8Cache / 1e6;
+    auto line8 = [&](const char* name, float us) { printf("| %s | %.2f | %.2f |\n", name, us, mb8 / us); };
+    printf("\n| q8_0 pattern (%.1f MB per layer) | us per layer | TB/s |\n|---|---|---|\n", mb8);
+    for (int pass = 0; pass < 2; ++pass) {
+        line8("1 KV head per workgroup (the decode plan at 16K), nontemporal",
+              time_layers([&](int l) { q8_pattern_kernel<1, true><<<256, 512>>>(ks[l], vs[l], out); }));
+        line8("1 KV head per workgroup, plain",
+              time_layers([&](int l) { q8_pattern_kernel<1, false><<<256, 512>>>(ks[l], vs[l], out); }));
+        line8("2 KV heads per workgroup, plain",
+              time_layers([&](int l) { q8_pattern_kernel<2, false><<<256, 512>>>(ks[l], vs[l], out); }));
+        line8("4 KV heads per workgroup, plain",
+              time_layers([&](int l) { q8_pattern_kernel<4, false><<<256, 512>>>(ks[l], vs[l], out); }));
+        line8("whole 1088-byte key rows, plain",
+              time_layers([&](int l) { q8_pattern_kernel<8, false><<<256, 512>>>(ks[l], vs[l], out); }));
     }
     const hipError_t e = hipDeviceSynchronize();
     if (e != hipSuccess) {
