@@ -110,6 +110,7 @@ enum DecodeStamp {
     kStampLdsMerged,      // every wave's state is in LDS
     kStampStored,         // the workgroup's partials are device-visible
     kStampArrived,        // the arrival counter returned
+    kStampIssued,         // last arrival: the loads of every split's partial are issued
     kStampLoaded,         // last arrival: every split's partial has been loaded
     kStampMerged,         // last arrival: the splits are merged
     kStampOut,            // last arrival: o is written
@@ -466,6 +467,7 @@ __device__ __forceinline__ void finish_split(const DecodeArgs<NS>& a, const SeqD
             for (int r = 0; r < kPer; ++r)
                 av[r] = ld_dev16(pa + (size_t)min(s0 + NSG * r, splits - 1) * kDim);
             mine = ld_dev8(pm + (size_t)min(s0 + NSG * ((threadIdx.x & (GL - 1)) % kPer), splits - 1) * 2);
+            DECODE_STAMP(kStampIssued);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             DECODE_STAMP(kStampLoaded);
 #pragma unroll

@@ -23,7 +23,7 @@ STAMPS = 16
 SLOTS = 8192
 PHASES = ["start", "first block in (wave 0)", "last block in (wave 0)", "wave 0 done",
           "all waves merged in LDS", "partials visible", "arrival counted",
-          "partials loaded (last)", "splits merged (last)", "o written (last)"]
+          "partial loads issued (last)", "partials loaded (last)", "splits merged (last)", "o written (last)"]
 
 
 def _load_trace_lib():
@@ -94,9 +94,9 @@ def run(lk: int, kv_name: str, reps: int = 5) -> dict:
             continue
         rows.append((name, v.size, v[0], v[v.size // 10], v[v.size // 2], v[v.size * 9 // 10],
                      v[-1]))
-    last = rel[np.isfinite(rel[:, 7])]
+    last = rel[np.isfinite(rel[:, PHASES.index("partials loaded (last)")])]
     return {"lk": lk, "kv": kv.name_str, "workgroups": int(used.sum()),
-            "us_per_layer": best, "phases": rows, "last": last[:, :10]}
+            "us_per_layer": best, "phases": rows, "last": last[:, :len(PHASES)]}
 
 
 def report(r: dict) -> str:
