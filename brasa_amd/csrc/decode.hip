@@ -336,24 +336,15 @@ constexpr int finish_floats() {
 //     else through LDS) are folded the same way, and o = A / L is written. The (m, l) pairs of a
 //     round are loaded once per group of lanes that share them and passed on through LDS. The
 //     order is fixed, so the result does not depend on which workgroup is last.
+// Steps 1-3 below for kernels that have written their wave states to `lds` themselves:
+// m_acc [W][G][128] (wave, head of the wave's head group, dim), then m_ml [W][G][2] (mref, lsum).
 template <int G, int W, int HPW, int NS>
-__device__ __forceinline__ void finish_split(const DecodeArgs<NS>& a, const SeqDesc& sd, int si,
-                                             int row, int split, float* lds,
-                                             const f32x4 (&acc)[8], float mref, float lsum) {
+__device__ __forceinline__ void finish_split_lds(const DecodeArgs<NS>& a, const SeqDesc& sd, int si,
+                                                 int row, int split, float* lds) {
     constexpr int KS = W / HPW;   // waves per head group
     constexpr int HG = HPW * G;   // query heads of the workgroup
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int c16 = lane & 15;
-    const int u = lane >> 4;
     float* m_acc = lds;                   // [W][G][128]
     float* m_ml = lds + W * G * kDim;     // [W][G][2]
-    if (c16 < G) {
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-            *reinterpret_cast<f32x4*>(m_acc + (wave * G + c16) * kDim + 16 * dt + 4 * u) = acc[dt];
-        if (u == 0) *reinterpret_cast<f32x2*>(m_ml + (wave * G + c16) * 2) = f32x2{mref, lsum};
-    }
     __syncthreads();
     DECODE_STAMP(kStampLdsMerged);
     const int splits = sd.splits;
@@ -534,6 +525,25 @@ __device__ __forceinline__ void finish_split(const DecodeArgs<NS>& a, const SeqD
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     DECODE_STAMP(kStampOut);
 #endif
+}
+
+template <int G, int W, int HPW, int NS>
+__device__ __forceinline__ void finish_split(const DecodeArgs<NS>& a, const SeqDesc& sd, int si,
+                                             int row, int split, float* lds,
+                                             const f32x4 (&acc)[8], float mref, float lsum) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int c16 = lane & 15;
+    const int u = lane >> 4;
+    float* m_acc = lds;                   // [W][G][128]
+    float* m_ml = lds + W * G * kDim;     // [W][G][2]
+    if (c16 < G) {
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+            *reinterpret_cast<f32x4*>(m_acc + (wave * G + c16) * kDim + 16 * dt + 4 * u) = acc[dt];
+        if (u == 0) *reinterpret_cast<f32x2*>(m_ml + (wave * G + c16) * 2) = f32x2{mref, lsum};
+    }
+    finish_split_lds<G, W, HPW>(a, sd, si, row, split, lds);
 }
 
 // ---- f32 caches (the reference's exact variant): register-staged K and V -------------------
@@ -1339,6 +1349,281 @@ decode_q8_kernel(DecodeArgs<NS> a) {
 }
 
 
+// ---- q8_0 caches, GQA group 4: the LDS copies above, cheaper block math -------------------
+// decode_q8h_kernel: decode_q8_kernel's workgroup, grid, copies (K and V codes and scales into
+// the wave's LDS ring slots, block i + 1 issued once block i has landed) and split merge, with
+// block math that needs no V tile rewrite, no factor table and no hi / lo split of P.
+// Lane l = (u = l / 16, c = l % 16), c = 4 gq + jh.
+//  * S^T = K Q^T on v_mfma_f32_16x16x32_f16, one k-step per 32-dim group t: the A operand is
+//    key c of the 16-key tile, dims 32 t + 8 u .. + 7 (codes exact in f16, read from LDS as in
+//    decode_q8_kernel); the B operand's 16 columns are the 4 query heads 4 times over (column c:
+//    head jh), Q * scale as f16 hi + lo in two chained MFMAs, so every lane ends with the
+//    scores of keys 4 u + r (r = 0..3) for its head jh. Each group's partial is scaled by the
+//    row's group scale in f32.
+//  * O += P V on v_mfma_f32_4x4x1_16b_f32 (16 blocks of 4 x 4, f32): block (u, gq) multiplies
+//    A = p(key, head jh) * vscale(key, group gq) (f32, one rounding) by B = the code of dim
+//    32 gq + 8 jh + e of the same key (exact f32, one sign-extending byte select), keys 4 u + r;
+//    P stays f32. Lane (u, c) reads its 8 codes of the key at byte 8 c of the row in LDS (lanes
+//    with u odd take the keys of a step in the order r ^ 1, so the four rows a read instruction
+//    touches fall in both halves of the banks). Accumulator e (0..7) holds, in lane (u, c),
+//    O[head 0..3][dim 32 gq + 8 jh + e] over the keys 4 u + r; the four u are summed at the
+//    wave's end.
+constexpr int kQ8hSlot = 2 * kQ8Codes + 2 * kBlock * 8;  // K codes, V codes, K scales, V scales
+
+template <int NS, int HPW, int W>
+__global__ void __launch_bounds__(64 * W)
+decode_q8h_kernel(DecodeArgs<NS> a) {
+    DECODE_STAMP(kStampStart);
+    constexpr int G = 4;
+    constexpr int RB = kQ8Row;
+    constexpr int KS = W / HPW;
+    static_assert(W <= kMaxLdsWaves, "waves per workgroup");
+    static_assert(finish_floats<G, W>() * 4 <= W * kRing * kQ8hSlot, "merge area in the ring");
+    __shared__ __attribute__((aligned(16))) uint8_t s_slot[W][kRing][kQ8hSlot];
+
+    const int rows = (a.ngroups + HPW - 1) / HPW;
+    int row, col;
+    xcd_grid_pos(rows, row, col);
+    const int si = seq_of(a, col);
+    const SeqDesc& sd = a.seq[si];
+    const int split = col - sd.split0;
+    const float* qseq = a.q + (size_t)si * a.hq * kDim;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR math
+    const int hl = wave % HPW, ks = wave / HPW;
+    const int hg = row * HPW + hl;
+    const bool hg_ok = hg < a.ngroups;
+    const int h0 = min(hg, a.ngroups - 1) * G;
+    const int kh = h0 / a.group;
+    const int c = lane & 15;
+    const int u = lane >> 4;
+    const int gq = c >> 2, jh = c & 3;
+    const int uo = u & 1;
+
+    const int s0 = split * sd.chunk;
+    const int s1 = min(sd.lk, s0 + sd.chunk);
+    const int nblk = (s1 - s0 + kBlock - 1) / kBlock;
+    const int nb = (hg_ok && nblk > ks) ? (nblk - ks + KS - 1) / KS : 0;
+    const size_t kstride = (size_t)a.hkv * RB;
+    const uint8_t* kbase = sgpr_base(sd.k + (size_t)kh * RB);
+    const uint8_t* vbase = sgpr_base(sd.v + (size_t)kh * RB);
+
+    u32x4 qr[8];
+    {
+        // column c: head h0 + jh; k-step t: dims 32 t + 8 u .. + 7
+        const uint8_t* qrow = reinterpret_cast<const uint8_t*>(qseq + (size_t)(h0 + jh) * kDim);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            qr[2 * t] = ld16_asm(qrow + 4 * (32 * t + 8 * u));
+            qr[2 * t + 1] = ld16_asm(qrow + 4 * (32 * t + 8 * u + 4));
+        }
+    }
+    // block i -> slot S, as decode_q8_kernel: K codes (4 instructions, 8 rows each, swizzled), V
+    // codes (4, swizzled), K scales, V scales (one 4-byte instruction each)
+    const int lr = lane >> 3, lc = lane & 7, sr = lane >> 1;
+    uint32_t off_k[4], off_v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int rr = 8 * r + lr;
+        off_k[r] = (uint32_t)(rr * kstride) + 16 * (lc ^ ((rr >> 1) & 7));
+        off_v[r] = (uint32_t)(rr * kstride) + 16 * (lc ^ q8_vswz(rr));
+    }
+    const uint32_t off_s = (uint32_t)(sr * kstride) + 128 + 4 * (lane & 1);
+    auto issue_at = [&](auto slot_c, int jb) {
+        constexpr int S = decltype(slot_c)::value;
+        const uint32_t sl = lds_addr(&s_slot[wave][S][0]);
+        const uint8_t* kb = sgpr_offset(kbase, (size_t)jb * kstride);
+        const uint8_t* vb = sgpr_offset(vbase, (size_t)jb * kstride);
+        if (jb + kBlock <= s1) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) lds_dma16_s(kb, off_k[r], sl + 1024 * r);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) lds_dma16_s(vb, off_v[r], sl + kQ8Codes + 1024 * r);
+            lds_dma4_s(kb, off_s, sl + 2 * kQ8Codes);
+            lds_dma4_s(vb, off_s, sl + 2 * kQ8Codes + 256);
+        } else {
+            const int last = s1 - 1 - jb;  // rows past it read the last row again
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int rr = 8 * r + lr;
+                const uint32_t rowo = (uint32_t)(min(rr, last) * kstride);
+                lds_dma16_s(kb, rowo + 16 * (lc ^ ((rr >> 1) & 7)), sl + 1024 * r);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int rr = 8 * r + lr;
+                const uint32_t rowo = (uint32_t)(min(rr, last) * kstride);
+                lds_dma16_s(vb, rowo + 16 * (lc ^ q8_vswz(rr)), sl + kQ8Codes + 1024 * r);
+            }
+            const uint32_t srow = (uint32_t)(min(sr, last) * kstride) + 128 + 4 * (lane & 1);
+            lds_dma4_s(kb, srow, sl + 2 * kQ8Codes);
+            lds_dma4_s(vb, srow, sl + 2 * kQ8Codes + 256);
+        }
+    };
+    auto issue = [&](auto slot_c, int i) { issue_at(slot_c, s0 + kBlock * (ks + KS * i)); };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    // one block in flight at the start (a wave without blocks copies the split's first one,
+    // never read), then one wait with a fixed count for the Q loads, as decode_q8_kernel
+    issue_at(I0{}, nb > 0 ? s0 + kBlock * ks : s0);
+    wait_k<10>(qr);
+
+    half8 qh[4], ql[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const f32x4 q0 = __builtin_bit_cast(f32x4, qr[2 * t]);
+        const f32x4 q1 = __builtin_bit_cast(f32x4, qr[2 * t + 1]);
+        const float sc = a.scale;
+        const float x[8] = {as_f32(q0.x * sc), as_f32(q0.y * sc), as_f32(q0.z * sc),
+                            as_f32(q0.w * sc), as_f32(q1.x * sc), as_f32(q1.y * sc),
+                            as_f32(q1.z * sc), as_f32(q1.w * sc)};  // f32, as reference
+        split8(x, qh[t], ql[t]);
+    }
+
+    float mref = -INFINITY;
+    float lsum = 0.0f;
+    f32x4 acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto step = [&](auto slot_c, int i) {
+        constexpr int S = decltype(slot_c)::value;
+        wait_vmcnt<0>();  // block i: the only copies in flight
+        if (i + 1 < nb) {
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the other slot's reads returned
+            asm volatile("" ::: "memory");
+            issue(std::integral_constant<int, 1 - S>{}, i + 1);
+        }
+        if (i == 0) DECODE_STAMP(kStampFirstBlock);
+        if (i + 1 == nb) DECODE_STAMP(kStampLastBlock);
+        const int jb = s0 + kBlock * (ks + KS * i);
+        const uint8_t* sl = &s_slot[wave][S][0];
+        const uint8_t* vco = sl + kQ8Codes;
+        const uint8_t* ksc = sl + 2 * kQ8Codes;
+        const uint8_t* vsc = sl + 2 * kQ8Codes + 256;
+        // this lane's V codes and V scales (keys 16 kt + 4 u + (r ^ uo)), read first: they return
+        // while S and the softmax are computed
+        u32x2 vw[2][4];
+        uint16_t vs[2][4];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int R = 16 * kt + 4 * u + (r ^ uo);
+                vw[kt][r] = *reinterpret_cast<const u32x2*>(vco + R * 128 + 16 * ((c >> 1) ^ q8_vswz(R)) + 8 * (c & 1));
+                vs[kt][r] = *reinterpret_cast<const uint16_t*>(vsc + R * 8 + 2 * gq);
+            }
+        // S^T: per 32-dim group t two chained MFMAs (Q hi, Q lo), scaled by the row's group scale
+        float x[2][4];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            const int r16 = 16 * kt + c;
+            f32x4 part[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int L = 2 * t + (u >> 1);
+                const u32x2 kc = *reinterpret_cast<const u32x2*>(sl + r16 * 128 + 16 * (L ^ ((r16 >> 1) & 7)) + 8 * (u & 1));
+                uint32_t l0, g0, l1, g1;
+                codes4_to_f16(kc.x, l0, g0);
+                codes4_to_f16(kc.y, l1, g1);
+                const half8 kf = as_half8(u32x4{l0, g0, l1, g1});
+                part[t] = mfma16(kf, ql[t], mfma16(kf, qh[t], f32x4{0.0f, 0.0f, 0.0f, 0.0f}));
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {  // scales of S row 16 kt + 4 u + r
+                const u32x2 sw = *reinterpret_cast<const u32x2*>(ksc + (16 * kt + 4 * u + r) * 8);
+                float v = part[0][r] * h2f((uint16_t)(sw.x & 0xffffu));
+                v = fmaf(part[1][r], h2f((uint16_t)(sw.x >> 16)), v);
+                v = fmaf(part[2][r], h2f((uint16_t)(sw.y & 0xffffu)), v);
+                v = fmaf(part[3][r], h2f((uint16_t)(sw.y >> 16)), v);
+                x[kt][r] = v * kLog2e;
+            }
+        }
+        if (jb + kBlock > s1) {  // the split's last block: keys past its end get -inf
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (jb + 16 * kt + 4 * u + r >= s1) x[kt][r] = -INFINITY;
+        }
+        float bm = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) bm = fmaxf(bm, x[kt][r]);
+        bm = max_rows(bm);
+        if (__builtin_amdgcn_ballot_w64(bm > mref + kLazyRescale) != 0) {
+            const float mn = fmaxf(mref, bm);
+            const float alpha = __builtin_amdgcn_exp2f(mref - mn);
+            mref = mn;
+            lsum *= alpha;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] *= alpha;
+        }
+        float p[2][4];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                p[kt][r] = __builtin_amdgcn_exp2f(x[kt][r] - mref);
+                lsum += p[kt][r];
+            }
+        // O += P V: the key of step r is 4 u + (r ^ uo), its p picked from the lane's own four
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float pk = uo ? p[kt][r ^ 1] : p[kt][r];
+                const float av = pk * h2f(vs[kt][r]);
+                const u32x2 w = vw[kt][r];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc[e] = __builtin_amdgcn_mfma_f32_4x4x1f32(
+                        av, (float)(int8_t)(w.x >> (8 * e)), acc[e], 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc[4 + e] = __builtin_amdgcn_mfma_f32_4x4x1f32(
+                        av, (float)(int8_t)(w.y >> (8 * e)), acc[4 + e], 0, 0, 0);
+            }
+    };
+    for (int i0 = 0; i0 < nb; i0 += kRing) {
+        step(I0{}, i0);
+        if (i0 + 1 >= nb) break;
+        step(I1{}, i0 + 1);
+    }
+    wait_vmcnt<0>();  // copies of a wave without blocks land before the LDS is reused below
+
+    // ---- the split's end: sum the key quarters u, lane (u, c) keeps head u ------------------
+    lsum = sum_rows(lsum);
+    float o8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        // lanes 0-31 keep heads 0 / 1, lanes 32-63 heads 2 / 3 (each summed over u and u ^ 2) ...
+        const auto s02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[e][0]),
+                                                          __float_as_uint(acc[e][2]), false, false);
+        const auto s13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[e][1]),
+                                                          __float_as_uint(acc[e][3]), false, false);
+        const float r0 = __uint_as_float(s02[0]) + __uint_as_float(s02[1]);
+        const float r1 = __uint_as_float(s13[0]) + __uint_as_float(s13[1]);
+        // ... then lanes with u even keep r0, odd r1 (summed over u and u ^ 1): head u
+        const auto s01 = __builtin_amdgcn_permlane16_swap(__float_as_uint(r0), __float_as_uint(r1),
+                                                          false, false);
+        o8[e] = __uint_as_float(s01[0]) + __uint_as_float(s01[1]);
+    }
+    __syncthreads();  // every wave is done with its slots (all copies waited for)
+    DECODE_STAMP(kStampWaveDone);
+    float* lds = reinterpret_cast<float*>(&s_slot[0][0][0]);
+    {
+        float* dst = lds + (wave * G + u) * kDim + 32 * gq + 8 * jh;  // m_acc [W][G][128]
+        *reinterpret_cast<f32x4*>(dst) = f32x4{o8[0], o8[1], o8[2], o8[3]};
+        *reinterpret_cast<f32x4*>(dst + 4) = f32x4{o8[4], o8[5], o8[6], o8[7]};
+        if (lane < G)  // m_ml [W][G][2]
+            *reinterpret_cast<f32x2*>(lds + W * G * kDim + (wave * G + jh) * 2) = f32x2{mref, lsum};
+    }
+    finish_split_lds<G, W, HPW>(a, sd, si, row, split, lds);
+}
+
+
 template <int KV> struct KernelFor;
 template <> struct KernelFor<BRASA_KV_F16> { static constexpr int W = kWavesF16; };
 template <> struct KernelFor<BRASA_KV_Q8_0> { static constexpr int W = kWavesQ8; };
@@ -1353,8 +1638,13 @@ int launch_hpw(const DecodeArgs<NS>& a, int cols, hipStream_t stream) {
         hipLaunchKernelGGL((decode_f16_kernel<G, NS, HPW, W>), grid, block, 0, stream, a);
         return check_launch("decode_f16_kernel");
     } else {
-        hipLaunchKernelGGL((decode_q8_kernel<G, NS, HPW, W>), grid, block, 0, stream, a);
-        return check_launch("decode_q8_kernel");
+        if constexpr (G == 4) {
+            hipLaunchKernelGGL((decode_q8h_kernel<NS, HPW, W>), grid, block, 0, stream, a);
+            return check_launch("decode_q8h_kernel");
+        } else {
+            hipLaunchKernelGGL((decode_q8_kernel<G, NS, HPW, W>), grid, block, 0, stream, a);
+            return check_launch("decode_q8_kernel");
+        }
     }
 }
 
