@@ -83,6 +83,7 @@ def run(lk: int, kv_name: str, reps: int = 5) -> dict:
         vb.free()
     t = t.reshape(SLOTS, STAMPS)
     used = t[:, 0] != 0                 # slots the launches wrote (one grid, every launch)
+    slot = np.nonzero(used)[0]          # = blockIdx.x (a single-sequence grid has < SLOTS)
     t = t[used]
     t0 = t[:, 0].min()
     rel = np.where(t >= t0, (t.astype(np.float64) - float(t0)) * 0.01, np.nan)  # us
@@ -95,8 +96,19 @@ def run(lk: int, kv_name: str, reps: int = 5) -> dict:
         rows.append((name, v.size, v[0], v[v.size // 10], v[v.size // 2], v[v.size * 9 // 10],
                      v[-1]))
     last = rel[np.isfinite(rel[:, PHASES.index("partials loaded (last)")])]
+    # per KV head: the fp16 kernel's grid has the head groups innermost (one head per workgroup
+    # at these lengths), so workgroup b reads KV head b % HKV
+    per_head = []
+    if kv.name_str == "f16":
+        col = PHASES.index("all waves merged in LDS")
+        for h in range(HKV):
+            v = rel[slot % HKV == h, col]
+            v = v[np.isfinite(v)]
+            if v.size:
+                per_head.append((h, v.size, float(np.median(v)), float(v.max())))
     return {"lk": lk, "kv": kv.name_str, "workgroups": int(used.sum()),
-            "us_per_layer": best, "phases": rows, "last": last[:, :len(PHASES)]}
+            "us_per_layer": best, "phases": rows, "last": last[:, :len(PHASES)],
+            "per_head": per_head}
 
 
 def report(r: dict) -> str:
@@ -111,6 +123,11 @@ def report(r: dict) -> str:
             "| " + " | ".join(PHASES) + " |", "|" + "---|" * len(PHASES)]
     for row in r["last"]:
         out.append("| " + " | ".join("" if not np.isfinite(x) else f"{x:.2f}" for x in row) + " |")
+    if r["per_head"]:
+        out += ["", "All waves of a workgroup merged in LDS, per KV head (us):", "",
+                "| KV head | workgroups | median | max |", "|---|---|---|---|"]
+        for h, n, med, mx in r["per_head"]:
+            out.append(f"| {h} | {n} | {med:.2f} | {mx:.2f} |")
     return "\n".join(out)
 
 
