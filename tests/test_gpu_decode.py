@@ -72,6 +72,26 @@ def test_decode_other_groups(kv):
         assert w <= 1e-5, (hq, w)
 
 
+@pytest.mark.parametrize("kv", KVS)
+def test_decode_partial_head_group_row(kv):
+    # six KV heads at GQA group 4: at short lengths the plan puts four head groups in a
+    # workgroup, so the second grid row holds two real head groups and two past the last one
+    # (waves without keys, merge threads past hq)
+    k = Kernels()
+    rng = oracle.Rng(31)
+    hq, hkv = 24, 6
+    w = 0.0
+    for pos0 in [0, 37, 300, 1024]:
+        lk = pos0 + 1
+        q = rng.vec(hq * DIM, 2.0)
+        cache = KvPair(kv, rng.vec(lk * hkv * DIM, 2.0), rng.vec(lk * hkv * DIM, 3.0))
+        _say(f"decode lanes hq={hq} hkv={hkv} kv={kv.name_str} pos0={pos0}")
+        got = run_decode(k, "lanes", q, cache, hq, hkv, pos0)
+        want, vmax = oracle.attention(q, cache.k, cache.v, 1, hq, hkv, DIM, pos0)
+        w = max(w, oracle.worst(got, want, vmax))
+    assert w <= 1e-5, w
+
+
 def test_decode_non_power_of_two_group():
     # group 3 is outside GQA_GROUPS: lanes is rejected (the reference panics), the per-head
     # variant serves it (lib.rs:1056-1103)
