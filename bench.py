@@ -375,7 +375,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the attention path has no "
-                                   "multi-GPU code (see DESIGN.md on sharding); run --gpus 1"}))
+                                   "multi-GPU code (it would shard by KV head, one GPU per head "
+                                   "group, with no communication); run --gpus 1"}))
         return 2
     stream = Stream()
     k = Kernels(stream)
