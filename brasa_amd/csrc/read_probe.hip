@@ -35,10 +35,13 @@ __device__ __forceinline__ u32x4 load16(const uint8_t* p) {
     return r;
 }
 
-// HPW heads per workgroup (1, 2, 4), or 8 for whole contiguous key rows.
-template <int HPW>
-__global__ void __launch_bounds__(512) pattern_kernel(const uint8_t* K, const uint8_t* V, unsigned* out) {
-    __shared__ __attribute__((aligned(16))) uint16_t s_v[8][2][4096];
+// HPW heads per workgroup (1, 2, 4), or 8 for whole contiguous key rows; W waves per workgroup
+// and 2048 / W workgroups (every wave reads 64 keys of one head). With W = 16 the two blocks of a
+// wave share one LDS slot (160 KB would not hold 16 x 2 x 8 KB): a timing probe only.
+template <int HPW, int W = 8>
+__global__ void __launch_bounds__(64 * W) pattern_kernel(const uint8_t* K, const uint8_t* V, unsigned* out) {
+    constexpr int kBlocks = W == 8 ? 2 : 1;
+    __shared__ __attribute__((aligned(16))) uint16_t s_v[W][kBlocks][4096];
     const int b = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int c16 = lane & 15, u = lane >> 4;
     u32x4 kx[2][8];
@@ -50,7 +53,7 @@ __global__ void __launch_bounds__(512) pattern_kernel(const uint8_t* K, const ui
             for (int kt = 0; kt < 2; ++kt) kr[kt] = K + base + (size_t)(16 * kt + c16) * kRow + 16 * u;
             for (int r = 0; r < 8; ++r) vr[r] = V + base + (size_t)(4 * r + u) * kRow + 16 * c16;
         } else {
-            constexpr int chunk = 512 / HPW, rows = 8 / HPW, per_head = 8 / HPW;
+            constexpr int rows = 8 / HPW, chunk = kKeys / (2048 / W / rows), per_head = W / HPW;
             const int row = b % rows, split = b / rows;
             const int head = row * HPW + w % HPW;
             const int key0 = chunk * split + 32 * (w / HPW + per_head * blk);
@@ -61,7 +64,7 @@ __global__ void __launch_bounds__(512) pattern_kernel(const uint8_t* K, const ui
         }
         for (int kt = 0; kt < 2; ++kt)
             for (int t = 0; t < 4; ++t) kx[blk][4 * kt + t] = load16(kr[kt] + 64 * t);
-        for (int r = 0; r < 8; ++r) lds_dma16_nt(vr[r], &s_v[w][blk][0] + 512 * r);
+        for (int r = 0; r < 8; ++r) lds_dma16_nt(vr[r], &s_v[w][blk % kBlocks][0] + 512 * r);
     }
     // every load has landed before a loaded register is read
     asm volatile("s_waitcnt vmcnt(0)"
@@ -72,9 +75,9 @@ __global__ void __launch_bounds__(512) pattern_kernel(const uint8_t* K, const ui
                  :
                  : "memory");
     __syncthreads();
-    unsigned x = s_v[w][0][lane] ^ s_v[w][1][lane];
+    unsigned x = s_v[w][0][lane] ^ s_v[w][kBlocks - 1][lane];
     for (int j = 0; j < 8; ++j) x ^= kx[0][j].x ^ kx[1][j].y;
-    if (lane == 0) out[b * 8 + w] = x;
+    if (lane == 0) out[b * W + w] = x;
 }
 
 __global__ void __launch_bounds__(256) stream_kernel(const uint8_t* K, const uint8_t* V, unsigned* out, int nwg) {
@@ -91,11 +94,11 @@ __global__ void __launch_bounds__(256) stream_kernel(const uint8_t* K, const uin
 // ---- q8_0 ------------------------------------------------------------------------------------
 constexpr size_t kQ8Cache = (size_t)kKeys * kHeads * kQ8Row;
 
-template <int HPW, bool NT>
-__global__ void __launch_bounds__(512) q8_pattern_kernel(const uint8_t* K, const uint8_t* V, unsigned* out) {
-    constexpr int rows = 8 / HPW, splits = 256 / rows, keys = kKeys / splits;
+template <int HPW, bool NT, int W = 8>
+__global__ void __launch_bounds__(64 * W) q8_pattern_kernel(const uint8_t* K, const uint8_t* V, unsigned* out) {
+    constexpr int rows = 8 / HPW, splits = 2048 / W / rows, keys = kKeys / splits;
     constexpr int seg = HPW * kQ8Row;           // bytes per position
-    constexpr int per_wave = keys * seg / 8;    // bytes per wave and cache
+    constexpr int per_wave = keys * seg / W;    // bytes per wave and cache
     constexpr int n = per_wave / 512;           // 8-byte loads per lane and cache
     static_assert(per_wave % 512 == 0, "whole wave loads");
     const int b = blockIdx.x, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -169,6 +172,10 @@ int main() {
              time_layers([&](int l) { pattern_kernel<4><<<256, 512>>>(ks[l], vs[l], out); }));
         line("whole 2 KB key rows",
              time_layers([&](int l) { pattern_kernel<8><<<256, 512>>>(ks[l], vs[l], out); }));
+        line("1 KV head per workgroup, 128 workgroups of 16 waves",
+             time_layers([&](int l) { pattern_kernel<1, 16><<<128, 1024>>>(ks[l], vs[l], out); }));
+        line("2 KV heads per workgroup, 128 workgroups of 16 waves",
+             time_layers([&](int l) { pattern_kernel<2, 16><<<128, 1024>>>(ks[l], vs[l], out); }));
         for (int nwg : {512, 1024, 4096}) {
             char name[64];
             snprintf(name, sizeof name, "stream, %d workgroups of 256", nwg);
@@ -188,6 +195,10 @@ int main() {
               time_layers([&](int l) { q8_pattern_kernel<2, false><<<256, 512>>>(ks[l], vs[l], out); }));
         line8("4 KV heads per workgroup, plain",
               time_layers([&](int l) { q8_pattern_kernel<4, false><<<256, 512>>>(ks[l], vs[l], out); }));
+        line8("1 KV head per workgroup, 128 workgroups of 16 waves, plain",
+              time_layers([&](int l) { q8_pattern_kernel<1, false, 16><<<128, 1024>>>(ks[l], vs[l], out); }));
+        line8("2 KV heads per workgroup, 128 workgroups of 16 waves, plain",
+              time_layers([&](int l) { q8_pattern_kernel<2, false, 16><<<128, 1024>>>(ks[l], vs[l], out); }));
         line8("whole 1088-byte key rows, plain",
               time_layers([&](int l) { q8_pattern_kernel<8, false><<<256, 512>>>(ks[l], vs[l], out); }));
     }
