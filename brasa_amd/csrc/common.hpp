@@ -258,20 +258,6 @@ __device__ __forceinline__ void lds_dma16_s(const uint8_t* sbase, uint32_t voff,
         : "v"(voff), "s"(sbase), "s"(lds_wave_base)
         : "memory");
 }
-// As lds_dma16_s with the nontemporal hint.
-__device__ __forceinline__ void lds_dma16_s_nt(const uint8_t* sbase, uint32_t voff,
-                                               uint32_t lds_wave_base /* uniform LDS address */) {
-    uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %3\n\t"
-        "s_nop 2\n\t"
-        "global_load_lds_dwordx4 %1, %2 nt\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(voff), "s"(sbase), "s"(lds_wave_base)
-        : "memory");
-}
 // 4-byte variant of lds_dma16_s (lane i writes lds + 4 i).
 __device__ __forceinline__ void lds_dma4_s(const uint8_t* sbase, uint32_t voff,
                                            uint32_t lds_wave_base /* uniform LDS address */) {
@@ -281,20 +267,6 @@ __device__ __forceinline__ void lds_dma4_s(const uint8_t* sbase, uint32_t voff,
         "s_mov_b32 m0, %3\n\t"
         "s_nop 2\n\t"
         "global_load_lds_dword %1, %2\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(voff), "s"(sbase), "s"(lds_wave_base)
-        : "memory");
-}
-// 4-byte variant of lds_dma16_s_nt (lane i writes lds + 4 i).
-__device__ __forceinline__ void lds_dma4_s_nt(const uint8_t* sbase, uint32_t voff,
-                                              uint32_t lds_wave_base /* uniform LDS address */) {
-    uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %3\n\t"
-        "s_nop 2\n\t"
-        "global_load_lds_dword %1, %2 nt\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
         : "v"(voff), "s"(sbase), "s"(lds_wave_base)
