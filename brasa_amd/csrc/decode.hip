@@ -817,9 +817,15 @@ decode_f16_kernel(DecodeArgs<NS> a) {
     const bool colq = c16 < G;
     const bool col_lo = col_is_lo<G>(c16);
 
-    const int s0 = split * sd.chunk;
-    const int s1 = min(sd.lk, s0 + sd.chunk);
-    const int nblk = (s1 - s0 + kBlock - 1) / kBlock;
+    // The split's keys: the 32-key blocks split, split + splits, split + 2 splits, ... of the
+    // sequence (the splits' blocks interleaved, so at any time the grid reads one region of the
+    // cache: a read of one head's rows per workgroup takes 13.2 us at 16K keys this way against
+    // 14.1 us with contiguous splits). Every split has at least one block (blocks >= splits since chunk >= 32),
+    // at most chunk / 32, and only the sequence's last block is partial.
+    const int s1 = sd.lk;
+    const int nblk = ((s1 + kBlock - 1) / kBlock - split + sd.splits - 1) / sd.splits;
+    const int bstride = kBlock * sd.splits;  // keys from one of the split's blocks to the next
+    const int s0 = kBlock * split;
     // this wave's blocks: ks, ks + KS, ...
     const int nb = (hg_ok && nblk > ks) ? (nblk - ks + KS - 1) / KS : 0;
     const size_t kstride = (size_t)a.hkv * RB;
@@ -842,7 +848,7 @@ decode_f16_kernel(DecodeArgs<NS> a) {
     // q stored at chunk c ^ 2 (q & 3))
     auto issue = [&](auto slot_c, int i) {
         constexpr int S = decltype(slot_c)::value;
-        const int jb = s0 + kBlock * (ks + KS * i);
+        const int jb = s0 + bstride * (ks + KS * i);
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
             const uint8_t* row = kbase + (size_t)min(jb + 16 * kt + c16, s1 - 1) * kstride + 16 * u;
@@ -899,7 +905,7 @@ decode_f16_kernel(DecodeArgs<NS> a) {
         else wait_k<0>(kr[S]);
         if (i == 0) DECODE_STAMP(kStampFirstBlock);
         if (i + 1 == nb) DECODE_STAMP(kStampLastBlock);
-        const int jb = s0 + kBlock * (ks + KS * i);
+        const int jb = s0 + bstride * (ks + KS * i);
         // the V^T operands, read from LDS now (the block has landed) so the reads return while
         // S^T and the softmax are computed (after the rescale branch they waited for them)
         const uint16_t* vt = &s_v[wave][S][0];
@@ -927,7 +933,7 @@ decode_f16_kernel(DecodeArgs<NS> a) {
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) x[kt][r] = (x[kt][r] + partner<G>(x[kt][r])) * kLog2e;
-        if (jb + kBlock > s1) {  // the split's last block: keys past its end get -inf
+        if (jb + kBlock > s1) {  // the sequence's last block: keys past its end get -inf
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt)
 #pragma unroll

@@ -38,7 +38,7 @@ __device__ __forceinline__ u32x4 load16(const uint8_t* p) {
 // HPW heads per workgroup (1, 2, 4), or 8 for whole contiguous key rows; W waves per workgroup
 // and 2048 / W workgroups (every wave reads 64 keys of one head). With W = 16 the two blocks of a
 // wave share one LDS slot (160 KB would not hold 16 x 2 x 8 KB): a timing probe only.
-template <int HPW, int W = 8>
+template <int HPW, int W = 8, bool XMIX = false, bool KIL = false>
 __global__ void __launch_bounds__(64 * W) pattern_kernel(const uint8_t* K, const uint8_t* V, unsigned* out) {
     constexpr int kBlocks = W == 8 ? 2 : 1;
     __shared__ __attribute__((aligned(16))) uint16_t s_v[W][kBlocks][4096];
@@ -54,9 +54,17 @@ __global__ void __launch_bounds__(64 * W) pattern_kernel(const uint8_t* K, const
             for (int r = 0; r < 8; ++r) vr[r] = V + base + (size_t)(4 * r + u) * kRow + 16 * c16;
         } else {
             constexpr int rows = 8 / HPW, chunk = kKeys / (2048 / W / rows), per_head = W / HPW;
-            const int row = b % rows, split = b / rows;
+            // XMIX: workgroups b, b + 8, ... (one XCD) take every row of a split in turn, so each
+            // XCD reads whole key rows of its splits; otherwise rows vary fastest (XCD = row)
+            const int j = b >> 3;
+            const int row = XMIX ? j % rows : b % rows;
+            const int split = XMIX ? (j / rows) * 8 + (b & 7) : b / rows;
             const int head = row * HPW + w % HPW;
-            const int key0 = chunk * split + 32 * (w / HPW + per_head * blk);
+            // KIL: a split's 32-key blocks interleaved with the other splits' (block i of split s
+            // is global block s + splits * i), so the workgroups read one region at a time
+            constexpr int splits = 2048 / W / rows;
+            const int bi = w / HPW + per_head * blk;
+            const int key0 = KIL ? 32 * (split + splits * bi) : chunk * split + 32 * bi;
             for (int kt = 0; kt < 2; ++kt)
                 kr[kt] = K + ((size_t)(key0 + 16 * kt + c16) * kHeads + head) * kRow + 16 * u;
             for (int r = 0; r < 8; ++r)
@@ -94,7 +102,7 @@ __global__ void __launch_bounds__(256) stream_kernel(const uint8_t* K, const uin
 // ---- q8_0 ------------------------------------------------------------------------------------
 constexpr size_t kQ8Cache = (size_t)kKeys * kHeads * kQ8Row;
 
-template <int HPW, bool NT, int W = 8>
+template <int HPW, bool NT, int W = 8, bool KIL = false>
 __global__ void __launch_bounds__(64 * W) q8_pattern_kernel(const uint8_t* K, const uint8_t* V, unsigned* out) {
     constexpr int rows = 8 / HPW, splits = 2048 / W / rows, keys = kKeys / splits;
     constexpr int seg = HPW * kQ8Row;           // bytes per position
@@ -107,7 +115,9 @@ __global__ void __launch_bounds__(64 * W) q8_pattern_kernel(const uint8_t* K, co
 #pragma unroll
     for (int i = 0; i < n; ++i) {
         const int byte = w * per_wave + i * 512 + lane * 8;
-        const size_t a = ((size_t)(key0 + byte / seg) * kHeads + row * HPW) * kQ8Row + byte % seg;
+        const int k = byte / seg;  // key within the split; KIL: 32-key blocks interleaved over the splits
+        const int key = KIL ? 32 * (b / rows + splits * (k / 32)) + k % 32 : key0 + k;
+        const size_t a = ((size_t)key * kHeads + row * HPW) * kQ8Row + byte % seg;
         if constexpr (NT) {
             xk[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(K + a));
             xv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(V + a));
@@ -166,6 +176,14 @@ int main() {
     for (int pass = 0; pass < 2; ++pass) {
         line("1 KV head per workgroup (the decode plan at 16K)",
              time_layers([&](int l) { pattern_kernel<1><<<256, 512>>>(ks[l], vs[l], out); }));
+        line("1 KV head per workgroup, 32-key blocks interleaved over the splits",
+             time_layers([&](int l) { pattern_kernel<1, 8, false, true><<<256, 512>>>(ks[l], vs[l], out); }));
+        line("2 KV heads per workgroup, 32-key blocks interleaved over the splits",
+             time_layers([&](int l) { pattern_kernel<2, 8, false, true><<<256, 512>>>(ks[l], vs[l], out); }));
+        line("1 KV head per workgroup, the heads of a split on one XCD",
+             time_layers([&](int l) { pattern_kernel<1, 8, true><<<256, 512>>>(ks[l], vs[l], out); }));
+        line("2 KV heads per workgroup, the heads of a split on one XCD",
+             time_layers([&](int l) { pattern_kernel<2, 8, true><<<256, 512>>>(ks[l], vs[l], out); }));
         line("2 KV heads per workgroup",
              time_layers([&](int l) { pattern_kernel<2><<<256, 512>>>(ks[l], vs[l], out); }));
         line("4 KV heads per workgroup",
@@ -191,6 +209,8 @@ int main() {
               time_layers([&](int l) { q8_pattern_kernel<1, true><<<256, 512>>>(ks[l], vs[l], out); }));
         line8("1 KV head per workgroup, plain",
               time_layers([&](int l) { q8_pattern_kernel<1, false><<<256, 512>>>(ks[l], vs[l], out); }));
+        line8("1 KV head per workgroup, plain, 32-key blocks interleaved over the splits",
+              time_layers([&](int l) { q8_pattern_kernel<1, false, 8, true><<<256, 512>>>(ks[l], vs[l], out); }));
         line8("2 KV heads per workgroup, plain",
               time_layers([&](int l) { q8_pattern_kernel<2, false><<<256, 512>>>(ks[l], vs[l], out); }));
         line8("4 KV heads per workgroup, plain",
