@@ -740,7 +740,7 @@ decode_f32_kernel(DecodeArgs<NS> a) {
 // computed.
 // Softmax: columns c < G hold the hi halves of the split Q / P operands, the partner columns
 // (col_is_lo) the lo halves; one DPP exchange adds them (the same bits in both lanes). Only the
-// split's last block masks keys past its end. The running max is lazy: the
+// sequence's last block masks keys past its end. The running max is lazy: the
 // reference point moves only when a block's max exceeds it by more than 2^8, so most blocks skip
 // the rescale of O.
 constexpr int kRing = 2;                    // blocks in flight per wave (16 instructions each)
@@ -1059,9 +1059,11 @@ decode_q8_kernel(DecodeArgs<NS> a) {
     const bool colq = c16 < G;
     const bool col_lo = col_is_lo<G>(c16);
 
-    const int s0 = split * sd.chunk;
-    const int s1 = min(sd.lk, s0 + sd.chunk);
-    const int nblk = (s1 - s0 + kBlock - 1) / kBlock;
+    // the split's 32-key blocks interleaved with the other splits', as in decode_f16_kernel
+    const int s1 = sd.lk;
+    const int nblk = ((s1 + kBlock - 1) / kBlock - split + sd.splits - 1) / sd.splits;
+    const int bstride = kBlock * sd.splits;
+    const int s0 = kBlock * split;
     const int nb = (hg_ok && nblk > ks) ? (nblk - ks + KS - 1) / KS : 0;
     const size_t kstride = (size_t)a.hkv * RB;
     const uint8_t* kbase = sgpr_base(sd.k + (size_t)kh * RB);
@@ -1123,7 +1125,7 @@ decode_q8_kernel(DecodeArgs<NS> a) {
             lds_dma4_s(vb, srow, sl + 2 * kQ8Codes + 256);
         }
     };
-    auto issue = [&](auto slot_c, int i) { issue_at(slot_c, s0 + kBlock * (ks + KS * i)); };
+    auto issue = [&](auto slot_c, int i) { issue_at(slot_c, s0 + bstride * (ks + KS * i)); };
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     // The prologue always issues one block (a wave without blocks copies the split's first one,
@@ -1133,7 +1135,7 @@ decode_q8_kernel(DecodeArgs<NS> a) {
     // has landed (in step i): with one block per wave in flight at the start, the first blocks
     // land earlier and block i's math overlaps block i + 1's copies (18.6 -> 18.3 us per layer
     // at 16K keys).
-    issue_at(I0{}, nb > 0 ? s0 + kBlock * ks : s0);
+    issue_at(I0{}, nb > 0 ? s0 + bstride * ks : s0);
     wait_k<10>(qr);
 
     half8 qb[4];
@@ -1171,7 +1173,7 @@ decode_q8_kernel(DecodeArgs<NS> a) {
         }
         if (i == 0) DECODE_STAMP(kStampFirstBlock);
         if (i + 1 == nb) DECODE_STAMP(kStampLastBlock);
-        const int jb = s0 + kBlock * (ks + KS * i);
+        const int jb = s0 + bstride * (ks + KS * i);
         uint8_t* sl = &s_slot[wave][S][0];
         const uint8_t* ksc = sl + 2 * kQ8Codes;
         const uint8_t* vsc = sl + 2 * kQ8Codes + 256;
@@ -1290,7 +1292,7 @@ decode_q8_kernel(DecodeArgs<NS> a) {
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) x[kt][r] = (x[kt][r] + partner<G>(x[kt][r])) * kLog2e;
-        if (jb + kBlock > s1) {  // the split's last block: keys past its end get -inf
+        if (jb + kBlock > s1) {  // the sequence's last block: keys past its end get -inf
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -1348,8 +1350,8 @@ decode_q8_kernel(DecodeArgs<NS> a) {
             // became separate moves with zeroed destinations
             asm volatile("" : "+v"(acc[dt][r]));
         }
-    __syncthreads();  // every wave is done with its slots (all copies waited for)
     DECODE_STAMP(kStampWaveDone);
+    __syncthreads();  // every wave is done with its slots (all copies waited for)
     finish_split<G, W, HPW>(a, sd, si, row, split, reinterpret_cast<float*>(&s_slot[0][0][0]),
                             acc, mref, lsum);
 }
@@ -1406,9 +1408,11 @@ decode_q8h_kernel(DecodeArgs<NS> a) {
     const int gq = c >> 2, jh = c & 3;
     const int uo = u & 1;
 
-    const int s0 = split * sd.chunk;
-    const int s1 = min(sd.lk, s0 + sd.chunk);
-    const int nblk = (s1 - s0 + kBlock - 1) / kBlock;
+    // the split's 32-key blocks interleaved with the other splits', as in decode_f16_kernel
+    const int s1 = sd.lk;
+    const int nblk = ((s1 + kBlock - 1) / kBlock - split + sd.splits - 1) / sd.splits;
+    const int bstride = kBlock * sd.splits;
+    const int s0 = kBlock * split;
     const int nb = (hg_ok && nblk > ks) ? (nblk - ks + KS - 1) / KS : 0;
     const size_t kstride = (size_t)a.hkv * RB;
     const uint8_t* kbase = sgpr_base(sd.k + (size_t)kh * RB);
@@ -1466,12 +1470,12 @@ decode_q8h_kernel(DecodeArgs<NS> a) {
             lds_dma4_s(vb, srow, sl + 2 * kQ8Codes + 256);
         }
     };
-    auto issue = [&](auto slot_c, int i) { issue_at(slot_c, s0 + kBlock * (ks + KS * i)); };
+    auto issue = [&](auto slot_c, int i) { issue_at(slot_c, s0 + bstride * (ks + KS * i)); };
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     // one block in flight at the start (a wave without blocks copies the split's first one,
     // never read), then one wait with a fixed count for the Q loads, as decode_q8_kernel
-    issue_at(I0{}, nb > 0 ? s0 + kBlock * ks : s0);
+    issue_at(I0{}, nb > 0 ? s0 + bstride * ks : s0);
     wait_k<10>(qr);
 
     half8 qh[4], ql[4];
@@ -1502,7 +1506,7 @@ decode_q8h_kernel(DecodeArgs<NS> a) {
         }
         if (i == 0) DECODE_STAMP(kStampFirstBlock);
         if (i + 1 == nb) DECODE_STAMP(kStampLastBlock);
-        const int jb = s0 + kBlock * (ks + KS * i);
+        const int jb = s0 + bstride * (ks + KS * i);
         const uint8_t* sl = &s_slot[wave][S][0];
         const uint8_t* vco = sl + kQ8Codes;
         const uint8_t* ksc = sl + 2 * kQ8Codes;
@@ -1545,7 +1549,7 @@ decode_q8h_kernel(DecodeArgs<NS> a) {
                 x[kt][r] = v * kLog2e;
             }
         }
-        if (jb + kBlock > s1) {  // the split's last block: keys past its end get -inf
+        if (jb + kBlock > s1) {  // the sequence's last block: keys past its end get -inf
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -1560,11 +1564,15 @@ decode_q8h_kernel(DecodeArgs<NS> a) {
         bm = max_rows(bm);
         if (__builtin_amdgcn_ballot_w64(bm > mref + kLazyRescale) != 0) {
             const float mn = fmaxf(mref, bm);
-            const float alpha = __builtin_amdgcn_exp2f(mref - mn);
+            const float alpha = __builtin_amdgcn_exp2f(mref - mn);  // of head jh
             mref = mn;
             lsum *= alpha;
+            // component h of every accumulator belongs to head h (the MFMA block's row), not
+            // to the lane's head jh: each gets the factor of lane jh = h of its quad
+            const f32x4 ah = f32x4{dpp<0x00>(alpha), dpp<0x55>(alpha), dpp<0xaa>(alpha),
+                                   dpp<0xff>(alpha)};
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] *= alpha;
+            for (int e = 0; e < 8; ++e) acc[e] *= ah;
         }
         float p[2][4];
 #pragma unroll
@@ -1616,8 +1624,8 @@ decode_q8h_kernel(DecodeArgs<NS> a) {
                                                           false, false);
         o8[e] = __uint_as_float(s01[0]) + __uint_as_float(s01[1]);
     }
-    __syncthreads();  // every wave is done with its slots (all copies waited for)
     DECODE_STAMP(kStampWaveDone);
+    __syncthreads();  // every wave is done with its slots (all copies waited for)
     float* lds = reinterpret_cast<float*>(&s_slot[0][0][0]);
     {
         float* dst = lds + (wave * G + u) * kDim + 32 * gq + 8 * jh;  // m_acc [W][G][128]

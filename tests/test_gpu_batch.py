@@ -70,3 +70,30 @@ def test_batch_other_groups(group):
     for i, lk in enumerate(lens):
         want, vmax = oracle.attention(qs[i], caches[i].k, caches[i].v, 1, hq, hkv, DIM, lk - 1)
         assert oracle.worst(got[i], want, vmax) <= 1e-5
+
+
+@pytest.mark.parametrize("kv", [KvType.F16, KvType.Q8_0])
+def test_ragged_batch_rescale_after_first_block(kv):
+    """The ragged batch (four adjacent KV heads per workgroup) on inputs whose scores jump
+    between blocks (test_gpu_decode.stepped_scores): rescales inside splits with a different
+    factor per query head."""
+    from test_gpu_decode import stepped_scores
+    lens = [int(x) for x in np.random.default_rng(12345).integers(1024, 16385, size=8)]
+    rng = np.random.default_rng(92)
+    data = [stepped_scores(rng, lk) for lk in lens]
+    caches = [KvPair(kv, kk, vv) for _, kk, vv in data]
+    q = DeviceBuffer.from_array(np.concatenate([d[0] for d in data]))
+    part = DeviceBuffer(4 * decode_batch_partials_len(HQ, lens))
+    o = DeviceBuffer(len(lens) * HQ * DIM * 4)
+    k = Kernels()
+    print(f"batch rescale kv={kv.name_str}", flush=True)
+    k.decode_attention_batch(q, [c.kbuf for c in caches], [c.vbuf for c in caches], lens, part,
+                             o, HQ, HKV, kv, OutDType.F32)
+    synchronize()
+    got = o.download(np.float32).reshape(len(lens), -1)
+    w = 0.0
+    for i, lk in enumerate(lens):
+        want, vmax = oracle.attention(data[i][0], caches[i].k, caches[i].v, 1, HQ, HKV, DIM, lk - 1)
+        w = max(w, oracle.worst(got[i], want, vmax))
+    print(f"ragged batch rescale KV {kv.name_str}: worst / max|v| = {w:.2e}")
+    assert w <= 1e-5, w

@@ -241,3 +241,45 @@ def test_decode_stream_without_counter_slot():
     want, vmax = oracle.attention(q, cache.k, cache.v, 1, HQ, HKV, DIM, pos0)
     assert oracle.worst(got, want, vmax) <= 1e-5
     assert np.max(np.abs(got - split)) <= 1e-5 * float(vmax.max())
+
+
+def stepped_scores(rng: np.random.Generator, lk: int, hq: int = HQ, hkv: int = HKV):
+    """Q / K / V whose scores jump between levels from one 32-key block to the next.
+
+    Every KV head has a unit direction d; K row j = 68 level(j // 32) d + noise with level in
+    {0, 1, 2, 3}, and query head h of that KV head is (1 + h % 4) d, so its scores sit near
+    6 (1 + h % 4) level nats. A wave whose next block is one level up sees its max grow by
+    ~8.7 log2 units (head factor 1) up to ~35 (factor 4): the lazy rescale of the running sum
+    runs after the first block, with a different factor for each query head of a group, and
+    the rescaled old part of the sum still weighs ~2^-8.7 for the factor-1 heads, so a wrong
+    factor shows far above the 1e-5 bar."""
+    g = hq // hkv
+    d = rng.standard_normal((hkv, DIM)).astype(np.float32)
+    d /= np.linalg.norm(d, axis=1, keepdims=True)
+    level = rng.integers(0, 4, size=(lk + 31) // 32).astype(np.float32)
+    lev = np.repeat(level, 32)[:lk]
+    k = 68.0 * lev[:, None, None] * d[None] + 0.05 * rng.standard_normal((lk, hkv, DIM))
+    v = rng.standard_normal((lk, hkv, DIM))
+    q = np.stack([(1 + h % 4) * d[h // g] for h in range(hq)])
+    return (q.astype(np.float32).reshape(-1), k.astype(np.float32).reshape(-1),
+            v.astype(np.float32).reshape(-1))
+
+
+@pytest.mark.parametrize("kv", KVS)
+def test_decode_rescale_after_first_block(kv):
+    """Scores that jump by 2^8.7 and more between blocks (stepped_scores): every kernel's lazy
+    rescale runs inside splits, once per query head with that head's own factor. The q8_0
+    group-4 kernel once scaled all four heads' accumulators by the lane's own head factor:
+    with these inputs that was 1.3e-4 max|v| off at pos0 700 (and 1.8 max|v| on one head group
+    of the seeded ragged batch once its keys were taken in another order)."""
+    k = Kernels()
+    rng = np.random.default_rng(91)
+    for pos0 in [700, 4095, 16383]:
+        q, kk, vv = stepped_scores(rng, pos0 + 1)
+        cache = KvPair(kv, kk, vv)
+        _say(f"decode rescale kv={kv.name_str} pos0={pos0}")
+        got = run_decode(k, "lanes", q, cache, HQ, HKV, pos0)
+        want, vmax = oracle.attention(q, cache.k, cache.v, 1, HQ, HKV, DIM, pos0)
+        w = oracle.worst(got, want, vmax)
+        print(f"decode rescale KV {kv.name_str} pos0 {pos0}: worst / max|v| = {w:.2e}")
+        assert w <= 1e-5, w
