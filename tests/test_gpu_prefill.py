@@ -462,3 +462,43 @@ def test_flash_key_split_chosen_by_size():
     a, r = bars(oracle.f16_to_f32(oh), ref16)
     print(f"auto key split: F16 max-abs {a:.2e} max-rel {r:.2e}")
     assert a <= 2e-3 and r <= 1e-2, (a, r)
+
+
+@pytest.mark.parametrize("kv", KVS)
+def test_flash_rescale_after_first_tile(kv):
+    """Scores that jump between 32-key blocks (test_gpu_decode.stepped_scores, every query token
+    with the same per-head factor): the lazy rescale runs after the first key tile with a
+    different factor for each query head; a wrong factor costs errors of ~1e-3 max|v| and more.
+    F16_PF32 holds the reference's 1e-5 bar. F32 is held at 2e-5 here: its Q (and f32 K)
+    operands are f16 hi + lo pairs with ~22 significant bits, so scores of up to ~70 nats carry
+    ~70 * 2^-22 = 1.7e-5 nats of error (measured 1.0-1.2e-5 max|v|); the random cases above stay
+    under 1e-5. F16 (P rounded to f16) holds the north-star bar against the Q-rounded reference
+    for f32 and f16 caches. With a q8_0 cache F16 takes K and V as f16(code * scale), whose
+    rounding moves these large scores by up to ~0.03 nats (measured max-abs 6.9e-3): reported,
+    not asserted."""
+    from test_gpu_decode import stepped_scores
+    k = Kernels()
+    rng = np.random.default_rng(93)
+    w_pf32 = w32 = mabs = mrel = 0.0
+    for tokens, pos0 in [(96, 0), (40, 700), (160, 2048)]:
+        lk = pos0 + tokens
+        cap = (lk + 63) // 64 * 64
+        q1, kk, vv = stepped_scores(rng, cap)
+        q = np.tile(q1, tokens)
+        cache = KvPair(kv, kk, vv)
+        ref16, vmax = oracle.attention(q, cache.k, cache.v, tokens, HQ, HKV, DIM, pos0, q16=True)
+        raw, _ = oracle.attention(q, cache.k, cache.v, tokens, HQ, HKV, DIM, pos0)
+        _say(f"prefill rescale kv={kv.name_str} T={tokens} pos0={pos0}")
+        oh = run_prefill(k, q, cache, tokens, HQ, HKV, pos0, PrefillPrecision.F16)
+        a, r = bars(oracle.f16_to_f32(oh), ref16)
+        mabs, mrel = max(mabs, a), max(mrel, r)
+        op = run_prefill(k, q, cache, tokens, HQ, HKV, pos0, PrefillPrecision.F16_PF32)
+        w_pf32 = max(w_pf32, oracle.worst_f16(op, ref16, vmax))
+        o32 = run_prefill(k, q, cache, tokens, HQ, HKV, pos0, PrefillPrecision.F32)
+        w32 = max(w32, oracle.worst(o32, raw, vmax))
+    print(f"flash rescale KV {kv.name_str}: F16 max-abs {mabs:.2e} max-rel {mrel:.2e}; "
+          f"F16_PF32 {w_pf32:.2e}; F32 {w32:.2e}")
+    assert w_pf32 <= 1e-5, w_pf32
+    assert w32 <= 2e-5, w32
+    if kv != KvType.Q8_0:
+        assert mabs <= 2e-3 and mrel <= 1e-2, (mabs, mrel)
