@@ -38,7 +38,7 @@ __device__ __forceinline__ u32x4 load16(const uint8_t* p) {
 // HPW heads per workgroup (1, 2, 4), or 8 for whole contiguous key rows; W waves per workgroup
 // and 2048 / W workgroups (every wave reads 64 keys of one head). With W = 16 the two blocks of a
 // wave share one LDS slot (160 KB would not hold 16 x 2 x 8 KB): a timing probe only.
-template <int HPW, int W = 8, bool XMIX = false, bool KIL = false>
+template <int HPW, int W = 8, bool XMIX = false, int KIL = 0>
 __global__ void __launch_bounds__(64 * W) pattern_kernel(const uint8_t* K, const uint8_t* V, unsigned* out) {
     constexpr int kBlocks = W == 8 ? 2 : 1;
     __shared__ __attribute__((aligned(16))) uint16_t s_v[W][kBlocks][4096];
@@ -64,7 +64,8 @@ __global__ void __launch_bounds__(64 * W) pattern_kernel(const uint8_t* K, const
             // is global block s + splits * i), so the workgroups read one region at a time
             constexpr int splits = 2048 / W / rows;
             const int bi = w / HPW + per_head * blk;
-            const int key0 = KIL ? 32 * (split + splits * bi) : chunk * split + 32 * bi;
+            // KIL = units of KIL blocks
+            const int key0 = KIL ? 32 * (KIL * (split + splits * (bi / KIL)) + bi % KIL) : chunk * split + 32 * bi;
             for (int kt = 0; kt < 2; ++kt)
                 kr[kt] = K + ((size_t)(key0 + 16 * kt + c16) * kHeads + head) * kRow + 16 * u;
             for (int r = 0; r < 8; ++r)
@@ -102,7 +103,7 @@ __global__ void __launch_bounds__(256) stream_kernel(const uint8_t* K, const uin
 // ---- q8_0 ------------------------------------------------------------------------------------
 constexpr size_t kQ8Cache = (size_t)kKeys * kHeads * kQ8Row;
 
-template <int HPW, bool NT, int W = 8, bool KIL = false>
+template <int HPW, bool NT, int W = 8, bool KIL = false, bool XCD = false>
 __global__ void __launch_bounds__(64 * W) q8_pattern_kernel(const uint8_t* K, const uint8_t* V, unsigned* out) {
     constexpr int rows = 8 / HPW, splits = 2048 / W / rows, keys = kKeys / splits;
     constexpr int seg = HPW * kQ8Row;           // bytes per position
@@ -110,13 +111,18 @@ __global__ void __launch_bounds__(64 * W) q8_pattern_kernel(const uint8_t* K, co
     constexpr int n = per_wave / 512;           // 8-byte loads per lane and cache
     static_assert(per_wave % 512 == 0, "whole wave loads");
     const int b = blockIdx.x, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int row = b % rows, key0 = (b / rows) * keys;
+    // XCD: the decode kernel's grid order (xcd_grid_pos: workgroups b, b + 8, ... on one XCD take
+    // the rows of a split in turn, so the heads of a split share their lines in one L2)
+    const int j = b >> 3;
+    const int row = XCD ? j % rows : b % rows;
+    const int split = XCD ? (j / rows) * 8 + (b & 7) : b / rows;
+    const int key0 = split * keys;
     u32x2 xk[n], xv[n];
 #pragma unroll
     for (int i = 0; i < n; ++i) {
         const int byte = w * per_wave + i * 512 + lane * 8;
         const int k = byte / seg;  // key within the split; KIL: 32-key blocks interleaved over the splits
-        const int key = KIL ? 32 * (b / rows + splits * (k / 32)) + k % 32 : key0 + k;
+        const int key = KIL ? 32 * (split + splits * (k / 32)) + k % 32 : key0 + k;
         const size_t a = ((size_t)key * kHeads + row * HPW) * kQ8Row + byte % seg;
         if constexpr (NT) {
             xk[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(K + a));
@@ -177,9 +183,13 @@ int main() {
         line("1 KV head per workgroup (the decode plan at 16K)",
              time_layers([&](int l) { pattern_kernel<1><<<256, 512>>>(ks[l], vs[l], out); }));
         line("1 KV head per workgroup, 32-key blocks interleaved over the splits",
-             time_layers([&](int l) { pattern_kernel<1, 8, false, true><<<256, 512>>>(ks[l], vs[l], out); }));
+             time_layers([&](int l) { pattern_kernel<1, 8, false, 1><<<256, 512>>>(ks[l], vs[l], out); }));
+        line("1 KV head per workgroup, 64-key units interleaved over the splits",
+             time_layers([&](int l) { pattern_kernel<1, 8, false, 2><<<256, 512>>>(ks[l], vs[l], out); }));
+        line("1 KV head per workgroup, 128-key units interleaved over the splits",
+             time_layers([&](int l) { pattern_kernel<1, 8, false, 4><<<256, 512>>>(ks[l], vs[l], out); }));
         line("2 KV heads per workgroup, 32-key blocks interleaved over the splits",
-             time_layers([&](int l) { pattern_kernel<2, 8, false, true><<<256, 512>>>(ks[l], vs[l], out); }));
+             time_layers([&](int l) { pattern_kernel<2, 8, false, 1><<<256, 512>>>(ks[l], vs[l], out); }));
         line("1 KV head per workgroup, the heads of a split on one XCD",
              time_layers([&](int l) { pattern_kernel<1, 8, true><<<256, 512>>>(ks[l], vs[l], out); }));
         line("2 KV heads per workgroup, the heads of a split on one XCD",
@@ -211,6 +221,10 @@ int main() {
               time_layers([&](int l) { q8_pattern_kernel<1, false><<<256, 512>>>(ks[l], vs[l], out); }));
         line8("1 KV head per workgroup, plain, 32-key blocks interleaved over the splits",
               time_layers([&](int l) { q8_pattern_kernel<1, false, 8, true><<<256, 512>>>(ks[l], vs[l], out); }));
+        line8("1 KV head per workgroup, plain, the decode kernel's XCD order",
+              time_layers([&](int l) { q8_pattern_kernel<1, false, 8, false, true><<<256, 512>>>(ks[l], vs[l], out); }));
+        line8("1 KV head per workgroup, plain, XCD order, 32-key blocks interleaved over the splits",
+              time_layers([&](int l) { q8_pattern_kernel<1, false, 8, true, true><<<256, 512>>>(ks[l], vs[l], out); }));
         line8("2 KV heads per workgroup, plain",
               time_layers([&](int l) { q8_pattern_kernel<2, false><<<256, 512>>>(ks[l], vs[l], out); }));
         line8("4 KV heads per workgroup, plain",
