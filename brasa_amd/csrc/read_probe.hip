@@ -138,6 +138,40 @@ __global__ void __launch_bounds__(64 * W) q8_pattern_kernel(const uint8_t* K, co
     if (acc.x == 0x9e3779b9u) out[b] = acc.y;  // keeps the loads
 }
 
+// The q8_0 decode kernel's own copies: per wave two 32-key blocks of one KV head, each 4 + 4
+// LDS-DMA copies of 16-byte code chunks and 2 of 4-byte scale pairs into the wave's LDS slots;
+// the decode kernel's grid order and interleaved blocks. BOTH: the two blocks issued at once;
+// otherwise block 1 only after block 0 has landed (the kernel's issue order), no math between.
+template <bool BOTH>
+__global__ void __launch_bounds__(512) q8_lds_kernel(const uint8_t* K, const uint8_t* V, unsigned* out) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_q8[8][2][8704];
+    const int b = blockIdx.x, lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR copy bases
+    const int j = b >> 3, row = j % 8, split = (j / 8) * 8 + (b & 7);
+    constexpr uint32_t kstride = kHeads * kQ8Row;
+    const uint8_t* kb0 = sgpr_base(K + row * kQ8Row);
+    const uint8_t* vb0 = sgpr_base(V + row * kQ8Row);
+    const int lr = lane >> 3, lc = lane & 7, sr = lane >> 1;
+    uint32_t off[4];
+    for (int r = 0; r < 4; ++r) off[r] = (uint32_t)((8 * r + lr) * kstride) + 16 * lc;
+    const uint32_t off_s = (uint32_t)(sr * kstride) + 128 + 4 * (lane & 1);
+    for (int blk = 0; blk < 2; ++blk) {
+        const int jb = 32 * (split + 32 * (w + 8 * blk));
+        const uint8_t* kb = sgpr_offset(kb0, (uint64_t)jb * kstride);
+        const uint8_t* vb = sgpr_offset(vb0, (uint64_t)jb * kstride);
+        const uint32_t sl = lds_addr(&s_q8[w][blk][0]);
+        for (int r = 0; r < 4; ++r) lds_dma16_s(kb, off[r], sl + 1024 * r);
+        for (int r = 0; r < 4; ++r) lds_dma16_s(vb, off[r], sl + 4096 + 1024 * r);
+        lds_dma4_s(kb, off_s, sl + 8192);
+        lds_dma4_s(vb, off_s, sl + 8448);
+        if (!BOTH && blk == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    const unsigned x = s_q8[w][0][4 * lane] ^ s_q8[w][1][4 * lane + 1];
+    if (x == 0x9e3779b9u) out[b] = x;
+}
+
 template <class F>
 float time_layers(F launch) {
     hipEvent_t e0, e1;
@@ -225,6 +259,10 @@ int main() {
               time_layers([&](int l) { q8_pattern_kernel<1, false, 8, false, true><<<256, 512>>>(ks[l], vs[l], out); }));
         line8("1 KV head per workgroup, plain, XCD order, 32-key blocks interleaved over the splits",
               time_layers([&](int l) { q8_pattern_kernel<1, false, 8, true, true><<<256, 512>>>(ks[l], vs[l], out); }));
+        line8("1 KV head per workgroup, the q8_0 kernel's LDS copies, both blocks at once",
+              time_layers([&](int l) { q8_lds_kernel<true><<<256, 512>>>(ks[l], vs[l], out); }));
+        line8("1 KV head per workgroup, the q8_0 kernel's LDS copies, block 1 after block 0 landed",
+              time_layers([&](int l) { q8_lds_kernel<false><<<256, 512>>>(ks[l], vs[l], out); }));
         line8("2 KV heads per workgroup, plain",
               time_layers([&](int l) { q8_pattern_kernel<2, false><<<256, 512>>>(ks[l], vs[l], out); }));
         line8("4 KV heads per workgroup, plain",
