@@ -502,3 +502,34 @@ def test_flash_rescale_after_first_tile(kv):
     assert w32 <= 2e-5, w32
     if kv != KvType.Q8_0:
         assert mabs <= 2e-3 and mrel <= 1e-2, (mabs, mrel)
+
+
+@pytest.mark.parametrize("kv", [KvType.F16, KvType.Q8_0])
+@pytest.mark.parametrize("variant,pair,parts,tokens,pos0", [
+    (1, 1, 1, 160, 700), (1, 0, 1, 160, 700), (1, 0, 3, 64, 4000), (2, 0, 1, 160, 700),
+    (4, 0, 1, 160, 700)])
+def test_flash_rescale_every_layout(kv, variant, pair, parts, tokens, pos0):
+    """test_flash_rescale_after_first_tile's stepped scores through each prefill kernel and
+    layout (two key groups with and without tile pairing, the key split, the four-wave and the
+    32-key-stage kernels; q8_0 rows staged as f16 for them): F16_PF32 at the reference's 1e-5
+    bar, F16 at the north-star bar for the f16 cache (reported for q8_0, as there)."""
+    from test_gpu_decode import stepped_scores
+    rng = np.random.default_rng(94)
+    lk = pos0 + tokens
+    cap = (lk + 63) // 64 * 64
+    q1, kk, vv = stepped_scores(rng, cap)
+    q = np.tile(q1, tokens)
+    cache = KvPair(kv, kk, vv)
+    _say(f"prefill rescale layout kv={kv.name_str} variant={variant} pair={pair} parts={parts}")
+    oh = run_prefill_layout(q, cache, tokens, HQ, HKV, pos0, PrefillPrecision.F16, variant, pair,
+                            parts)
+    op = run_prefill_layout(q, cache, tokens, HQ, HKV, pos0, PrefillPrecision.F16_PF32, variant,
+                            pair, parts)
+    ref16, vmax = oracle.attention(q, cache.k, cache.v, tokens, HQ, HKV, DIM, pos0, q16=True)
+    a, r = bars(oracle.f16_to_f32(oh), ref16)
+    w = oracle.worst_f16(op, ref16, vmax)
+    print(f"rescale layout {kv.name_str} {variant}/{pair}/{parts}: F16 max-abs {a:.2e} "
+          f"max-rel {r:.2e}; F16_PF32 worst_f16 {w:.2e}")
+    assert w <= 1e-5, w
+    if kv == KvType.F16:
+        assert a <= 2e-3 and r <= 1e-2, (a, r)
