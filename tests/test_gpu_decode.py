@@ -283,3 +283,22 @@ def test_decode_rescale_after_first_block(kv):
         w = oracle.worst(got, want, vmax)
         print(f"decode rescale KV {kv.name_str} pos0 {pos0}: worst / max|v| = {w:.2e}")
         assert w <= 1e-5, w
+
+
+@pytest.mark.parametrize("kv", KVS)
+@pytest.mark.parametrize("hq,hkv,variant", [(32, 32, "lanes"), (32, 16, "lanes"), (64, 8, "lanes"),
+                                            (32, 8, "per_head")])
+def test_decode_rescale_other_groups(kv, hq, hkv, variant):
+    """stepped_scores at GQA groups 1, 2 and 8 (the generic q8_0 kernel, other head-group
+    layouts) and through the per-head decode_attention: the reference's 1e-5 bar."""
+    k = Kernels()
+    rng = np.random.default_rng(95)
+    pos0 = 4095
+    q, kk, vv = stepped_scores(rng, pos0 + 1, hq, hkv)
+    cache = KvPair(kv, kk, vv)
+    _say(f"decode rescale kv={kv.name_str} hq={hq} hkv={hkv} {variant}")
+    got = run_decode(k, variant, q, cache, hq, hkv, pos0)
+    want, vmax = oracle.attention(q, cache.k, cache.v, 1, hq, hkv, DIM, pos0)
+    w = oracle.worst(got, want, vmax)
+    print(f"decode rescale KV {kv.name_str} hq {hq} hkv {hkv} {variant}: worst / max|v| = {w:.2e}")
+    assert w <= 1e-5, w
