@@ -38,13 +38,13 @@ __device__ __forceinline__ u32x4 load16(const uint8_t* p) {
 // HPW heads per workgroup (1, 2, 4), or 8 for whole contiguous key rows; W waves per workgroup
 // and 2048 / W workgroups (every wave reads 64 keys of one head). With W = 16 the two blocks of a
 // wave share one LDS slot (160 KB would not hold 16 x 2 x 8 KB): a timing probe only.
-template <int HPW, int W = 8, bool XMIX = false, int KIL = 0>
+template <int HPW, int W = 8, bool XMIX = false, int KIL = 0, bool VREG = false>
 __global__ void __launch_bounds__(64 * W) pattern_kernel(const uint8_t* K, const uint8_t* V, unsigned* out) {
     constexpr int kBlocks = W == 8 ? 2 : 1;
     __shared__ __attribute__((aligned(16))) uint16_t s_v[W][kBlocks][4096];
     const int b = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int c16 = lane & 15, u = lane >> 4;
-    u32x4 kx[2][8];
+    u32x4 kx[2][8], vx[2][8];
     for (int blk = 0; blk < 2; ++blk) {
         const uint8_t *kr[2], *vr[8];
         if constexpr (HPW == 8) {
@@ -73,7 +73,12 @@ __global__ void __launch_bounds__(64 * W) pattern_kernel(const uint8_t* K, const
         }
         for (int kt = 0; kt < 2; ++kt)
             for (int t = 0; t < 4; ++t) kx[blk][4 * kt + t] = load16(kr[kt] + 64 * t);
-        for (int r = 0; r < 8; ++r) lds_dma16_nt(vr[r], &s_v[w][blk % kBlocks][0] + 512 * r);
+        if constexpr (VREG) {
+            // VREG: the V rows into registers too (plain 16-byte loads), no LDS copy
+            for (int r = 0; r < 8; ++r) vx[blk][r] = load16(vr[r]);
+        } else {
+            for (int r = 0; r < 8; ++r) lds_dma16_nt(vr[r], &s_v[w][blk % kBlocks][0] + 512 * r);
+        }
     }
     // every load has landed before a loaded register is read
     asm volatile("s_waitcnt vmcnt(0)"
@@ -83,9 +88,19 @@ __global__ void __launch_bounds__(64 * W) pattern_kernel(const uint8_t* K, const
                    "+v"(kx[1][7])
                  :
                  : "memory");
+    if constexpr (VREG)  // names the V registers too: no use of them above the wait
+        asm volatile("s_waitcnt vmcnt(0)"
+                     : "+v"(vx[0][0]), "+v"(vx[0][1]), "+v"(vx[0][2]), "+v"(vx[0][3]), "+v"(vx[0][4]),
+                       "+v"(vx[0][5]), "+v"(vx[0][6]), "+v"(vx[0][7]), "+v"(vx[1][0]), "+v"(vx[1][1]),
+                       "+v"(vx[1][2]), "+v"(vx[1][3]), "+v"(vx[1][4]), "+v"(vx[1][5]), "+v"(vx[1][6]),
+                       "+v"(vx[1][7])
+                     :
+                     : "memory");
     __syncthreads();
     unsigned x = s_v[w][0][lane] ^ s_v[w][kBlocks - 1][lane];
     for (int j = 0; j < 8; ++j) x ^= kx[0][j].x ^ kx[1][j].y;
+    if constexpr (VREG)
+        for (int j = 0; j < 8; ++j) x ^= vx[0][j].z ^ vx[1][j].w;
     if (lane == 0) out[b * W + w] = x;
 }
 
@@ -218,6 +233,8 @@ int main() {
              time_layers([&](int l) { pattern_kernel<1><<<256, 512>>>(ks[l], vs[l], out); }));
         line("1 KV head per workgroup, 32-key blocks interleaved over the splits",
              time_layers([&](int l) { pattern_kernel<1, 8, false, 1><<<256, 512>>>(ks[l], vs[l], out); }));
+        line("1 KV head per workgroup, interleaved 32-key blocks, V into registers (no LDS copy)",
+             time_layers([&](int l) { pattern_kernel<1, 8, false, 1, true><<<256, 512>>>(ks[l], vs[l], out); }));
         line("1 KV head per workgroup, 64-key units interleaved over the splits",
              time_layers([&](int l) { pattern_kernel<1, 8, false, 2><<<256, 512>>>(ks[l], vs[l], out); }));
         line("1 KV head per workgroup, 128-key units interleaved over the splits",
