@@ -59,6 +59,10 @@ SYMBOLS = {
     "brasa_test_flash_attention_layout": (INT, [VP, VP, VP, VP, AttnShapeC, INT, INT, INT, INT,
                                                 VP]),
     "brasa_test_stream_slot": (INT, [INT, VP, ctypes.POINTER(INT)]),
+    "brasa_test_decode_plan": (INT, [VP, INT, INT, INT, INT, ctypes.POINTER(INT),
+                                     ctypes.POINTER(INT), VP]),
+    "brasa_test_split_blocks": (INT, [INT, INT, INT, ctypes.POINTER(INT), ctypes.POINTER(INT),
+                                      ctypes.POINTER(INT)]),
     "brasa_release_workspaces": (INT, []),
     "brasa_last_error": (ctypes.c_char_p, []),
     "brasa_version": (ctypes.c_char_p, []),

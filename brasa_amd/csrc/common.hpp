@@ -40,6 +40,21 @@ struct DecodePlan {
 };
 DecodePlan decode_plan(const int* lk, int n, int ngroups, int G, int kv);
 
+// The 32-key blocks of split `split` of a sequence of lk keys cut into `splits` splits: blocks
+// split, split + splits, split + 2 splits, ... of the sequence, interleaved with the other splits'
+// so that at any time the grid reads one region of the cache. `first` is the first block's key,
+// `stride` the keys from one of the split's blocks to the next, `count` its blocks (at least one
+// whenever blocks >= splits; only the sequence's last block can be partial).
+struct SplitBlocks {
+    int first;
+    int stride;
+    int count;
+};
+__host__ __device__ inline SplitBlocks split_blocks(int lk, int splits, int split) {
+    const int nblocks = (lk + 31) / 32;
+    return SplitBlocks{32 * split, 32 * splits, (nblocks - split + splits - 1) / splits};
+}
+
 // ---- f16 helpers --------------------------------------------------------------------------
 __device__ __forceinline__ float h2f(uint16_t h) {
     return static_cast<float>(__ushort_as_half(h));

@@ -822,10 +822,11 @@ decode_f16_kernel(DecodeArgs<NS> a) {
     // cache: a read of one head's rows per workgroup takes 13.2 us at 16K keys this way against
     // 14.1 us with contiguous splits). Every split has at least one block (blocks >= splits since chunk >= 32),
     // at most chunk / 32, and only the sequence's last block is partial.
+    const SplitBlocks sb = split_blocks(sd.lk, sd.splits, split);
     const int s1 = sd.lk;
-    const int nblk = ((s1 + kBlock - 1) / kBlock - split + sd.splits - 1) / sd.splits;
-    const int bstride = kBlock * sd.splits;  // keys from one of the split's blocks to the next
-    const int s0 = kBlock * split;
+    const int nblk = sb.count;
+    const int bstride = sb.stride;  // keys from one of the split's blocks to the next
+    const int s0 = sb.first;
     // this wave's blocks: ks, ks + KS, ...
     const int nb = (hg_ok && nblk > ks) ? (nblk - ks + KS - 1) / KS : 0;
     const size_t kstride = (size_t)a.hkv * RB;
@@ -1060,10 +1061,11 @@ decode_q8_kernel(DecodeArgs<NS> a) {
     const bool col_lo = col_is_lo<G>(c16);
 
     // the split's 32-key blocks interleaved with the other splits', as in decode_f16_kernel
+    const SplitBlocks sb = split_blocks(sd.lk, sd.splits, split);
     const int s1 = sd.lk;
-    const int nblk = ((s1 + kBlock - 1) / kBlock - split + sd.splits - 1) / sd.splits;
-    const int bstride = kBlock * sd.splits;
-    const int s0 = kBlock * split;
+    const int nblk = sb.count;
+    const int bstride = sb.stride;
+    const int s0 = sb.first;
     const int nb = (hg_ok && nblk > ks) ? (nblk - ks + KS - 1) / KS : 0;
     const size_t kstride = (size_t)a.hkv * RB;
     const uint8_t* kbase = sgpr_base(sd.k + (size_t)kh * RB);
@@ -1409,10 +1411,11 @@ decode_q8h_kernel(DecodeArgs<NS> a) {
     const int uo = u & 1;
 
     // the split's 32-key blocks interleaved with the other splits', as in decode_f16_kernel
+    const SplitBlocks sb = split_blocks(sd.lk, sd.splits, split);
     const int s1 = sd.lk;
-    const int nblk = ((s1 + kBlock - 1) / kBlock - split + sd.splits - 1) / sd.splits;
-    const int bstride = kBlock * sd.splits;
-    const int s0 = kBlock * split;
+    const int nblk = sb.count;
+    const int bstride = sb.stride;
+    const int s0 = sb.first;
     const int nb = (hg_ok && nblk > ks) ? (nblk - ks + KS - 1) / KS : 0;
     const size_t kstride = (size_t)a.hkv * RB;
     const uint8_t* kbase = sgpr_base(sd.k + (size_t)kh * RB);
@@ -1888,3 +1891,25 @@ extern "C" int brasa_decode_trace_read(unsigned long long* dst, size_t n) {
     return e == hipSuccess ? 0 : BRASA_ERR_LAUNCH;
 }
 #endif
+
+extern "C" int brasa_test_decode_plan(const int* lk, int n, int hq, int hkv, int kv, int* chunk,
+                                      int* hpw, int* splits) {
+    if (!lk || n <= 0 || n > 64 || hkv <= 0 || hq % hkv != 0 || !chunk || !hpw || !splits)
+        return brasa::set_error(BRASA_ERR_ARG, "test_decode_plan: bad arguments");
+    const brasa::DecodePlan p = brasa::decode_plan(lk, n, hkv, hq / hkv, kv);
+    *chunk = p.chunk;
+    *hpw = p.hpw;
+    for (int i = 0; i < n; ++i) splits[i] = (lk[i] + p.chunk - 1) / p.chunk;
+    return BRASA_OK;
+}
+
+extern "C" int brasa_test_split_blocks(int lk, int splits, int split, int* first, int* stride,
+                                       int* count) {
+    if (lk <= 0 || splits <= 0 || split < 0 || split >= splits || !first || !stride || !count)
+        return brasa::set_error(BRASA_ERR_ARG, "test_split_blocks: bad arguments");
+    const brasa::SplitBlocks b = brasa::split_blocks(lk, splits, split);
+    *first = b.first;
+    *stride = b.stride;
+    *count = b.count;
+    return BRASA_OK;
+}

@@ -326,6 +326,18 @@ int brasa_test_flash_attention_layout(const float* q, const void* k, const void*
  */
 int brasa_test_stream_slot(int device, void* stream, int* slot);
 
+/*
+ * Test hooks (no counterpart in the reference). brasa_test_decode_plan: the decode launch plan
+ * for n <= 64 sequences of lengths lk (as one batched launch on a stream with a counter slot
+ * plans it): keys per split, head groups per workgroup, and each sequence's split count.
+ * brasa_test_split_blocks: the 32-key blocks split `split` of a sequence of lk keys in `splits`
+ * splits computes (the kernels' own function): the first block's key, the keys between its
+ * blocks and their count. Need no GPU.
+ */
+int brasa_test_decode_plan(const int* lk, int n, int hq, int hkv, int kv, int* chunk, int* hpw,
+                           int* splits);
+int brasa_test_split_blocks(int lk, int splits, int split, int* first, int* stride, int* count);
+
 #ifdef BRASA_TIMELINE_BUILD
 /*
  * Timeline build only (libbrasa_attn_trace.so; no counterpart in the reference): copy up to n

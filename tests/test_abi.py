@@ -291,3 +291,50 @@ def test_prefill_workspace_len():
         16896 * 8 * 128 * 2 * 2 + 128 * 2 * 4 * 17 * 64 * 16
     assert wl(AttnShape(0, 32, 8, 128, 0, KvType.F16), F16) == 0
     assert wl(AttnShape(16, 32, 8, 64, 0, KvType.F16), F16) == 0  # invalid shape
+
+
+def _plan(lens, hq=32, hkv=8, kv=KvType.F16):
+    from brasa_amd._lib import check
+    arr = (ctypes.c_int * len(lens))(*lens)
+    splits = (ctypes.c_int * len(lens))()
+    chunk, hpw = ctypes.c_int(), ctypes.c_int()
+    check(lib().brasa_test_decode_plan(arr, len(lens), hq, hkv, int(kv), ctypes.byref(chunk),
+                                       ctypes.byref(hpw), splits))
+    return chunk.value, hpw.value, list(splits)
+
+
+def _blocks(lk, splits, split):
+    from brasa_amd._lib import check
+    f, st, n = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    check(lib().brasa_test_split_blocks(lk, splits, split, ctypes.byref(f), ctypes.byref(st),
+                                        ctypes.byref(n)))
+    return [f.value + st.value * i for i in range(n.value)]
+
+
+@pytest.mark.parametrize("lens,hq,hkv,kv", [
+    ([1], 32, 8, KvType.F16), ([37], 32, 8, KvType.Q8_0), ([128], 32, 8, KvType.F16),
+    ([129], 32, 8, KvType.F16), ([2048], 32, 8, KvType.F16), ([4096], 32, 8, KvType.Q8_0),
+    ([5889], 32, 8, KvType.F16), ([16384], 32, 8, KvType.F16), ([16384], 32, 8, KvType.Q8_0),
+    ([32768], 32, 8, KvType.F16), ([131072], 32, 8, KvType.F16), ([16384], 32, 32, KvType.F16),
+    ([4095], 64, 8, KvType.F32),
+    ([11764, 4516, 13138, 5889, 4160, 13272, 10896, 11411], 32, 8, KvType.F16),
+    ([11764, 4516, 13138, 5889, 4160, 13272, 10896, 11411], 32, 8, KvType.Q8_0),
+    ([1, 2, 37, 64, 65, 127, 128, 129, 300, 1025, 3000] * 5 + [5, 999, 2048, 17], 32, 8,
+     KvType.F16)])
+def test_decode_splits_partition_the_keys(lens, hq, hkv, kv):
+    """The decode plan and the kernels' split_blocks, called through the library: for every
+    sequence, the splits' 32-key blocks (interleaved: block s + S i of split s) cover each of its
+    blocks exactly once, every split has at least one block and at most chunk / 32, the split
+    count stays within the reference-sized scratch (ceil(lk / 128) splits), chunks are multiples
+    of 32 keys and at least 128, and only the sequence's last block reaches past lk."""
+    chunk, hpw, splits = _plan(lens, hq, hkv, kv)
+    assert chunk % 32 == 0 and chunk >= 128 and hpw in (1, 2, 4)
+    for lk, s in zip(lens, splits):
+        assert s == -(-lk // chunk) and s <= -(-lk // 128)
+        seen = []
+        for sp in range(s):
+            b = _blocks(lk, s, sp)
+            assert 1 <= len(b) <= chunk // 32, (lk, s, sp, len(b))
+            assert all(k % 32 == 0 and k < lk for k in b)
+            seen += b
+        assert sorted(seen) == list(range(0, lk, 32)), lk
