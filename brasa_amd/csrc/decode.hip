@@ -595,9 +595,11 @@ decode_f32_kernel(DecodeArgs<NS> a) {
         qb[t] = col_lo ? lo : hi;
     }
 
-    const int s0 = split * sd.chunk;
-    const int s1 = min(sd.lk, s0 + sd.chunk);
-    const int nblk = (s1 - s0 + kBlock - 1) / kBlock;
+    // the split's 32-key blocks interleaved with the other splits' (split_blocks)
+    const SplitBlocks sb = split_blocks(sd.lk, sd.splits, split);
+    const int s0 = sb.first;
+    const int s1 = sd.lk;
+    const int nblk = sb.count;
     const int nb = nblk > wave ? (nblk - wave + W - 1) / W : 0;  // this wave's blocks
     const size_t kstride = (size_t)a.hkv * RB;
     const uint8_t* kbase = sd.k + (size_t)kh * RB;
@@ -700,7 +702,7 @@ decode_f32_kernel(DecodeArgs<NS> a) {
 
     // ---- stream this wave's 32-key blocks, the next block's loads in flight -----------------
     if (nb > 0) {
-        auto blk = [&](int i) { return s0 + kBlock * (wave + W * i); };
+        auto blk = [&](int i) { return s0 + sb.stride * (wave + W * i); };
         F32Block A, B;
         load(A, blk(0));
         // the prefetch is unconditional (rows clamp to s1 - 1): a branch around it would make
