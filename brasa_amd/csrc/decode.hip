@@ -1488,10 +1488,10 @@ decode_q8h_kernel(DecodeArgs<NS> a) {
     for (int t = 0; t < 4; ++t) {
         const f32x4 q0 = __builtin_bit_cast(f32x4, qr[2 * t]);
         const f32x4 q1 = __builtin_bit_cast(f32x4, qr[2 * t + 1]);
-        const float sc = a.scale;
+        const float sc = a.scale * kLog2e;  // scores come out in the log2 domain
         const float x[8] = {as_f32(q0.x * sc), as_f32(q0.y * sc), as_f32(q0.z * sc),
                             as_f32(q0.w * sc), as_f32(q1.x * sc), as_f32(q1.y * sc),
-                            as_f32(q1.z * sc), as_f32(q1.w * sc)};  // f32, as reference
+                            as_f32(q1.z * sc), as_f32(q1.w * sc)};  // f32: q * (scale log2 e)
         split8(x, qh[t], ql[t]);
     }
 
@@ -1547,11 +1547,11 @@ decode_q8h_kernel(DecodeArgs<NS> a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {  // scales of S row 16 kt + 4 u + r
                 const u32x2 sw = *reinterpret_cast<const u32x2*>(ksc + (16 * kt + 4 * u + r) * 8);
-                float v = part[0][r] * h2f((uint16_t)(sw.x & 0xffffu));
+                float v = fmaf(part[0][r], h2f((uint16_t)(sw.x & 0xffffu)), 0.0f);  // one mixed FMA
                 v = fmaf(part[1][r], h2f((uint16_t)(sw.x >> 16)), v);
                 v = fmaf(part[2][r], h2f((uint16_t)(sw.y & 0xffffu)), v);
                 v = fmaf(part[3][r], h2f((uint16_t)(sw.y >> 16)), v);
-                x[kt][r] = v * kLog2e;
+                x[kt][r] = v;
             }
         }
         if (jb + kBlock > s1) {  // the sequence's last block: keys past its end get -inf
@@ -1593,7 +1593,7 @@ decode_q8h_kernel(DecodeArgs<NS> a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float pk = uo ? p[kt][r ^ 1] : p[kt][r];
-                const float av = pk * h2f(vs[kt][r]);
+                const float av = fmaf(pk, h2f(vs[kt][r]), 0.0f);  // one mixed FMA
                 const u32x2 w = vw[kt][r];
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
