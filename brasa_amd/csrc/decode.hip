@@ -879,14 +879,14 @@ decode_f16_kernel(DecodeArgs<NS> a) {
     // its partner column (col_is_lo): the same head, lo half; other columns zero ------------------
     half8 qb[4];
     {
-        const float sc = (colq || col_lo) ? a.scale : 0.0f;
+        const float sc = (colq || col_lo) ? a.scale * kLog2e : 0.0f;  // scores in the log2 domain
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const f32x4 q0 = __builtin_bit_cast(f32x4, qr[2 * t]);
             const f32x4 q1 = __builtin_bit_cast(f32x4, qr[2 * t + 1]);
             const float x[8] = {as_f32(q0.x * sc), as_f32(q0.y * sc), as_f32(q0.z * sc),
                                 as_f32(q0.w * sc), as_f32(q1.x * sc), as_f32(q1.y * sc),
-                                as_f32(q1.z * sc), as_f32(q1.w * sc)};  // f32, as reference
+                                as_f32(q1.z * sc), as_f32(q1.w * sc)};  // f32: q * (scale log2 e)
             half8 hi, lo;
             split8(x, hi, lo);
             qb[t] = col_lo ? lo : hi;
@@ -935,7 +935,7 @@ decode_f16_kernel(DecodeArgs<NS> a) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) x[kt][r] = (x[kt][r] + partner<G>(x[kt][r])) * kLog2e;
+            for (int r = 0; r < 4; ++r) x[kt][r] = x[kt][r] + partner<G>(x[kt][r]);
         if (jb + kBlock > s1) {  // the sequence's last block: keys past its end get -inf
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt)
